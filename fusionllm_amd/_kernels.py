@@ -1,0 +1,247 @@
+"""Python wrappers of the libfusionmoe entry points (one per C function).
+
+Each wrapper checks shapes, dtypes, contiguity and device on the host,
+allocates the outputs with torch (device memory and streams are PyTorch's;
+the kernels run on the current stream), calls the C ABI and raises on a
+nonzero status.  Nothing here computes on the CPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import functools
+
+import torch
+
+from . import _lib
+from ._lib import BF16, F32, check, ptr_array
+
+# Optional per-entry-point timing: when a dict is installed with
+# set_timer(), every wrapper records a pair of HIP events around its launches
+# on the current stream (the stream the kernels run on) and appends them
+# under its name.  Used by bench.py; off by default.
+_TIMER: dict | None = None
+
+
+def set_timer(store: dict | None) -> None:
+    global _TIMER
+    _TIMER = store
+
+
+def _timed(fn):
+    name = fn.__name__
+
+    @functools.wraps(fn)
+    def wrapper(*args, tag: str | None = None, **kwargs):
+        if _TIMER is None:
+            return fn(*args, **kwargs)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        out = fn(*args, **kwargs)
+        end.record()
+        _TIMER.setdefault(name if tag is None else f"{name}:{tag}", []).append((start, end))
+        return out
+    return wrapper
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _req(t: torch.Tensor, name: str, dtype: torch.dtype | None = None) -> int:
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a ROCm device tensor (got {t.device})")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+    if dtype is not None and t.dtype != dtype:
+        raise RuntimeError(f"{name} must be {dtype} (got {t.dtype})")
+    return t.data_ptr()
+
+
+def _dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.bfloat16:
+        return BF16
+    if dt == torch.float32:
+        return F32
+    raise RuntimeError(f"unsupported dtype {dt}")
+
+
+@_timed
+def router_fwd(x, gate_w, gate_b, k: int, route_scale: float):
+    """fp32-logit biased-sigmoid top-k routing; returns idx32, idx64, weights, topv."""
+    lib = _lib.load()
+    T, d = x.shape
+    E = gate_w.shape[0]
+    dev = x.device
+    idx = torch.empty(T, k, dtype=torch.int32, device=dev)
+    idx64 = torch.empty(T, k, dtype=torch.int64, device=dev)
+    w = torch.empty(T, k, dtype=torch.float32, device=dev)
+    v = torch.empty(T, k, dtype=torch.float32, device=dev)
+    check(lib.fmoe_router_fwd(_req(x, "x", torch.bfloat16), _req(gate_w, "gate.weight", torch.bfloat16),
+                              _req(gate_b, "gate.bias", torch.bfloat16), T, d, E, k, float(route_scale),
+                              idx.data_ptr(), idx64.data_ptr(), w.data_ptr(), v.data_ptr(), _stream()),
+          "fmoe_router_fwd")
+    return idx, idx64, w, v
+
+
+@_timed
+def dispatch(idx, x, n_experts: int, gather: bool = True):
+    """Histogram + scan + stable scatter (+ row gather); returns counts, offsets, perm, pos, x_perm."""
+    lib = _lib.load()
+    T, k = idx.shape
+    d = x.shape[1]
+    dev = x.device
+    counts = torch.empty(n_experts, dtype=torch.int32, device=dev)
+    offsets = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(T * k, dtype=torch.int32, device=dev)
+    pos = torch.empty(T * k, dtype=torch.int32, device=dev)
+    x_perm = torch.empty(T * k, d, dtype=torch.bfloat16, device=dev) if gather else None
+    ws_bytes = lib.fmoe_dispatch_workspace_bytes(T, n_experts, k)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    check(lib.fmoe_dispatch(_req(idx, "idx", torch.int32), _req(x, "x", torch.bfloat16), T, d, n_experts, k,
+                            counts.data_ptr(), offsets.data_ptr(), perm.data_ptr(), pos.data_ptr(),
+                            x_perm.data_ptr() if x_perm is not None else None,
+                            ws.data_ptr(), ws_bytes, _stream()),
+          "fmoe_dispatch")
+    return counts, offsets, perm, pos, x_perm
+
+
+@_timed
+def gateup_fwd(x_perm, x_shared, offsets, n_experts: int, w1s, w3s, inter: int):
+    lib = _lib.load()
+    rows_r, d = x_perm.shape
+    rows_s = x_shared.shape[0] if x_shared is not None else 0
+    dev = x_perm.device
+    rows = rows_r + rows_s
+    ab = torch.empty(rows, 2 * inter, dtype=torch.bfloat16, device=dev)
+    h = torch.empty(rows, inter, dtype=torch.bfloat16, device=dev)
+    check(lib.fmoe_gateup_fwd(_req(x_perm, "x_perm", torch.bfloat16),
+                              _req(x_shared, "x", torch.bfloat16) if x_shared is not None else None,
+                              _req(offsets, "offsets", torch.int32), n_experts, rows_r, rows_s, d, inter,
+                              ptr_array([w.data_ptr() for w in w1s]), ptr_array([w.data_ptr() for w in w3s]),
+                              ab.data_ptr(), h.data_ptr(), _stream()),
+          "fmoe_gateup_fwd")
+    return ab, h
+
+
+@_timed
+def down_fwd(h, offsets, n_experts: int, rows_routed: int, rows_shared: int, w2s, dim: int):
+    lib = _lib.load()
+    rows, inter = h.shape
+    out = torch.empty(rows, dim, dtype=torch.bfloat16, device=h.device)
+    check(lib.fmoe_down_fwd(_req(h, "h", torch.bfloat16), _req(offsets, "offsets", torch.int32), n_experts,
+                            rows_routed, rows_shared, dim, inter, ptr_array([w.data_ptr() for w in w2s]),
+                            out.data_ptr(), _stream()),
+          "fmoe_down_fwd")
+    return out
+
+
+@_timed
+def combine_fwd(expert_out, idx, weights, pos, rows_routed: int, has_shared: bool, out_dtype: torch.dtype):
+    lib = _lib.load()
+    T, k = idx.shape
+    d = expert_out.shape[1]
+    y = torch.empty(T, d, dtype=out_dtype, device=expert_out.device)
+    check(lib.fmoe_combine_fwd(_req(expert_out, "expert_out", torch.bfloat16), _req(idx, "idx", torch.int32),
+                               _req(weights, "weights", torch.float32), _req(pos, "pos_of_slot", torch.int32),
+                               T, d, k, rows_routed, int(has_shared), _dtype_code(out_dtype), y.data_ptr(),
+                               _stream()),
+          "fmoe_combine_fwd")
+    return y
+
+
+@_timed
+def combine_bwd(dy, expert_out, weights, perm, k: int):
+    lib = _lib.load()
+    T, d = dy.shape
+    d_eo = torch.empty(T * k, d, dtype=torch.bfloat16, device=dy.device)
+    d_w = torch.empty(T, k, dtype=torch.float32, device=dy.device)
+    check(lib.fmoe_combine_bwd(_req(dy, "dy"), _dtype_code(dy.dtype), _req(expert_out, "expert_out", torch.bfloat16),
+                               _req(weights, "weights", torch.float32), _req(perm, "perm", torch.int32),
+                               T, d, k, d_eo.data_ptr(), d_w.data_ptr(), _stream()),
+          "fmoe_combine_bwd")
+    return d_eo, d_w
+
+
+@_timed
+def down_bwd_dx(d_out_routed, d_out_shared, offsets, n_experts: int, w2s, ab, inter: int):
+    lib = _lib.load()
+    rows_r, d = d_out_routed.shape
+    rows_s = d_out_shared.shape[0] if d_out_shared is not None else 0
+    d_ab = torch.empty(rows_r + rows_s, 2 * inter, dtype=torch.bfloat16, device=ab.device)
+    check(lib.fmoe_down_bwd_dx(_req(d_out_routed, "d_out", torch.bfloat16),
+                               _req(d_out_shared, "d_out_shared", torch.bfloat16) if d_out_shared is not None else None,
+                               _req(offsets, "offsets", torch.int32), n_experts, rows_r, rows_s, d, inter,
+                               ptr_array([w.data_ptr() for w in w2s]), _req(ab, "ab", torch.bfloat16),
+                               d_ab.data_ptr(), _stream()),
+          "fmoe_down_bwd_dx")
+    return d_ab
+
+
+@_timed
+def gateup_bwd_dx(d_ab, offsets, n_experts: int, rows_routed: int, rows_shared: int, w1s, w3s, dim: int):
+    lib = _lib.load()
+    rows, two_i = d_ab.shape
+    dx_rows = torch.empty(rows, dim, dtype=torch.bfloat16, device=d_ab.device)
+    check(lib.fmoe_gateup_bwd_dx(_req(d_ab, "d_ab", torch.bfloat16), _req(offsets, "offsets", torch.int32),
+                                 n_experts, rows_routed, rows_shared, dim, two_i // 2,
+                                 ptr_array([w.data_ptr() for w in w1s]), ptr_array([w.data_ptr() for w in w3s]),
+                                 dx_rows.data_ptr(), _stream()),
+          "fmoe_gateup_bwd_dx")
+    return dx_rows
+
+
+@_timed
+def weight_grad(a_routed, a_shared, b_routed, b_shared, offsets, n_experts: int, rows_routed: int,
+                rows_shared: int, m_split: int, outs_lo, outs_hi, out_dtype: torch.dtype):
+    """G_e = A_e^T B_e for every group, written into outs_lo[e] / outs_hi[e]."""
+    lib = _lib.load()
+    m_out = a_routed.shape[1]
+    n_out = b_routed.shape[1]
+    ws_bytes = lib.fmoe_weight_grad_workspace_bytes(rows_routed, rows_shared, n_experts, m_out, n_out)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=a_routed.device)
+    lo = ptr_array([o.data_ptr() for o in outs_lo])
+    hi = ptr_array([o.data_ptr() for o in outs_hi]) if outs_hi is not None else None
+    check(lib.fmoe_weight_grad(_req(a_routed, "A", torch.bfloat16),
+                               _req(a_shared, "A_shared", torch.bfloat16) if a_shared is not None else None,
+                               a_routed.stride(0),
+                               _req(b_routed, "B", torch.bfloat16),
+                               _req(b_shared, "B_shared", torch.bfloat16) if b_shared is not None else None,
+                               b_routed.stride(0),
+                               _req(offsets, "offsets", torch.int32), n_experts, rows_routed, rows_shared,
+                               m_out, n_out, m_split, lo, hi, _dtype_code(out_dtype),
+                               ws.data_ptr(), ws_bytes, _stream()),
+          "fmoe_weight_grad")
+
+
+@_timed
+def router_bwd(d_w, topv, perm, offsets, x_perm, n_experts: int, route_scale: float, grad_dtype: torch.dtype):
+    lib = _lib.load()
+    T, k = d_w.shape
+    d = x_perm.shape[1]
+    dev = d_w.device
+    d_logits = torch.empty(T, k, dtype=torch.float32, device=dev)
+    dgw = torch.empty(n_experts, d, dtype=grad_dtype, device=dev)
+    dgb = torch.empty(n_experts, dtype=grad_dtype, device=dev)
+    ws_bytes = lib.fmoe_router_bwd_workspace_bytes(T, d, n_experts, k)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    check(lib.fmoe_router_bwd(_req(d_w, "d_weights", torch.float32), _req(topv, "topv", torch.float32),
+                              _req(perm, "perm", torch.int32), _req(offsets, "offsets", torch.int32),
+                              _req(x_perm, "x_perm", torch.bfloat16), T, d, n_experts, k, float(route_scale),
+                              d_logits.data_ptr(), dgw.data_ptr(), dgb.data_ptr(), _dtype_code(grad_dtype),
+                              ws.data_ptr(), ws_bytes, _stream()),
+          "fmoe_router_bwd")
+    return d_logits, dgw, dgb
+
+
+@_timed
+def dx_reduce(dx_rows, pos, idx, d_logits, gate_w, rows_routed: int, has_shared: bool, out_dtype: torch.dtype):
+    lib = _lib.load()
+    T, k = idx.shape
+    d = dx_rows.shape[1]
+    dx = torch.empty(T, d, dtype=out_dtype, device=dx_rows.device)
+    check(lib.fmoe_dx_reduce(_req(dx_rows, "dx_rows", torch.bfloat16), _req(pos, "pos_of_slot", torch.int32),
+                             _req(idx, "idx", torch.int32), _req(d_logits, "d_logits", torch.float32),
+                             _req(gate_w, "gate.weight", torch.bfloat16), T, d, k, rows_routed, int(has_shared),
+                             _dtype_code(out_dtype), dx.data_ptr(), _stream()),
+          "fmoe_dx_reduce")
+    return dx

@@ -1,0 +1,18 @@
+// abi.hip — version and status-string entry points of libfusionmoe.so.
+#include "fmoe_common.h"
+
+extern "C" int fmoe_abi_version(void) { return FMOE_ABI_VERSION; }
+
+extern "C" const char* fmoe_status_string(int status) {
+  switch (status) {
+    case FMOE_OK: return "ok";
+    case FMOE_ERR_INVALID_ARG: return "invalid argument (null pointer or negative size)";
+    case FMOE_ERR_SHAPE: return "unsupported shape (dim and inter must be multiples of 64, k <= min(E, 8))";
+    case FMOE_ERR_ALIGN: return "pointer or leading dimension not 16-byte aligned";
+    case FMOE_ERR_DTYPE: return "unknown dtype code";
+    case FMOE_ERR_LAUNCH: return "kernel launch failed";
+    case FMOE_ERR_WORKSPACE: return "workspace smaller than the size query returned";
+    case FMOE_ERR_TOO_MANY_EXPERTS: return "number of experts outside 1..64";
+    default: return "unknown status";
+  }
+}

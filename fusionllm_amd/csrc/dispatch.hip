@@ -1,0 +1,184 @@
+// dispatch.hip — expert histogram, exclusive scan, stable counting-sort
+// scatter and row gather.
+//
+// Replaces the permutation half of DeepSeekMoE._dispatch_scatter_gather,
+// FusionLLM models/moe.py:55-64 (flatten, argsort, unique_consecutive,
+// cumsum) and the per-expert gathers x[token_ids] (moe.py:73,75).  The
+// reference sorts with torch.argsort (moe.py:58); this is a counting sort
+// whose order is expert-major and slot-ascending inside each expert, the
+// order of a stable argsort.  Nothing is copied to the host: the counts and
+// offsets stay in device memory for the grouped GEMMs.
+//
+// Slots are processed in blocks of kSlotsPerBlock.  Stage 1 counts each
+// block's slots per expert; stage 2 (one workgroup) turns the block counts
+// into each block's first row per expert; stage 3 ranks each slot among the
+// earlier slots of its block with the same expert (wave ballots, then an
+// exclusive prefix over the waves of the block) and writes perm /
+// pos_of_slot.  Stage 4 copies rows of x into the expert-contiguous buffer
+// with 16-byte loads and stores, many rows per workgroup.
+#include "fmoe_common.h"
+
+namespace fmoe {
+
+constexpr int kDispThreads = 256;
+constexpr int kDispWaves = kDispThreads / 64;
+constexpr int kSlotsPerThread = 4;
+constexpr int kSlotsPerBlock = kDispThreads * kSlotsPerThread;
+
+__global__ __launch_bounds__(kDispThreads) void dispatch_hist_kernel(
+    const int32_t* __restrict__ idx, int n_slots, int E, int32_t* __restrict__ block_hist) {
+  __shared__ int cnt[FMOE_MAX_EXPERTS];
+  for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
+  __syncthreads();
+  const int base = blockIdx.x * kSlotsPerBlock;
+#pragma unroll
+  for (int i = 0; i < kSlotsPerThread; ++i) {
+    const int s = base + i * kDispThreads + threadIdx.x;
+    if (s < n_slots) {
+      const int e = idx[s];
+      if (static_cast<unsigned>(e) < static_cast<unsigned>(E)) atomicAdd(&cnt[e], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x)
+    block_hist[static_cast<int64_t>(blockIdx.x) * E + e] = cnt[e];
+}
+
+// One workgroup.  block_base[b][e] = offsets[e] + sum_{b' < b} block_hist[b'][e].
+__global__ __launch_bounds__(64) void dispatch_scan_kernel(
+    const int32_t* __restrict__ block_hist, int nblocks, int E, int32_t* __restrict__ block_base,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets) {
+  __shared__ int total[FMOE_MAX_EXPERTS];
+  __shared__ int start[FMOE_MAX_EXPERTS + 1];
+  const int e = threadIdx.x;
+  if (e < E) {
+    int run = 0;
+    for (int b = 0; b < nblocks; ++b) {
+      const int64_t o = static_cast<int64_t>(b) * E + e;
+      const int h = block_hist[o];
+      block_base[o] = run;
+      run += h;
+    }
+    total[e] = run;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int q = 0; q < E; ++q) { start[q] = run; run += total[q]; }
+    start[E] = run;
+  }
+  __syncthreads();
+  if (e < E) {
+    counts[e] = total[e];
+    offsets[e] = start[e];
+    for (int b = 0; b < nblocks; ++b) block_base[static_cast<int64_t>(b) * E + e] += start[e];
+  }
+  if (e == 0) offsets[E] = start[E];
+}
+
+__global__ __launch_bounds__(kDispThreads) void dispatch_scatter_kernel(
+    const int32_t* __restrict__ idx, int n_slots, int E, const int32_t* __restrict__ block_base,
+    int32_t* __restrict__ perm, int32_t* __restrict__ pos_of_slot) {
+  __shared__ int running[FMOE_MAX_EXPERTS];
+  __shared__ int wcount[kDispWaves][FMOE_MAX_EXPERTS];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  for (int e = threadIdx.x; e < E; e += blockDim.x)
+    running[e] = block_base[static_cast<int64_t>(blockIdx.x) * E + e];
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int round = 0; round < kSlotsPerThread; ++round) {
+    for (int i = threadIdx.x; i < kDispWaves * E; i += blockDim.x) wcount[i / E][i % E] = 0;
+    __syncthreads();
+    const int s = blockIdx.x * kSlotsPerBlock + round * kDispThreads + threadIdx.x;
+    const int e_raw = s < n_slots ? idx[s] : -1;
+    const bool valid = static_cast<unsigned>(e_raw) < static_cast<unsigned>(E);
+    const int e = valid ? e_raw : -1;
+    // Rank among lanes of this wave with the same expert (lower lanes first).
+    uint64_t pending = __ballot(valid);
+    int rank = 0;
+    while (pending) {
+      const int leader = __ffsll(static_cast<unsigned long long>(pending)) - 1;
+      const int le = __shfl(e, leader);
+      const uint64_t m = __ballot(e == le);
+      if (e == le) rank = __popcll(m & lt_mask);
+      if (lane == leader) wcount[wave][le] = __popcll(m);
+      pending &= ~m;
+    }
+    __syncthreads();
+    if (valid) {
+      int pos = running[e] + rank;
+      for (int w = 0; w < wave; ++w) pos += wcount[w][e];
+      if (pos >= 0 && pos < n_slots) {  // always true for expert ids in range
+        perm[pos] = s;
+        pos_of_slot[s] = pos;
+      }
+    }
+    __syncthreads();
+    for (int q = threadIdx.x; q < E; q += blockDim.x) {
+      int add = 0;
+      for (int w = 0; w < kDispWaves; ++w) add += wcount[w][q];
+      running[q] += add;
+    }
+    __syncthreads();
+  }
+}
+
+// x_perm[r] = x[perm[r] / k]: one 16-byte chunk per thread.
+__global__ __launch_bounds__(256) void dispatch_gather_kernel(
+    const int32_t* __restrict__ perm, const uint4* __restrict__ x, int64_t n_rows, int chunks,
+    int k, uint4* __restrict__ x_perm) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (g >= n_rows * chunks) return;
+  const int64_t r = g / chunks;
+  const int c = static_cast<int>(g - r * chunks);
+  const int64_t slot = perm[r];
+  if (slot < 0 || slot >= n_rows) return;  // perm holds slots 0 .. n_rows-1
+  x_perm[g] = x[(slot / k) * chunks + c];
+}
+
+}  // namespace fmoe
+
+using namespace fmoe;
+
+extern "C" size_t fmoe_dispatch_workspace_bytes(int64_t T, int n_experts, int k) {
+  if (T <= 0 || n_experts <= 0 || k <= 0) return 0;
+  const int64_t nblocks = ceil_div(T * k, kSlotsPerBlock);
+  return static_cast<size_t>(2 * nblocks * n_experts) * sizeof(int32_t);
+}
+
+extern "C" int fmoe_dispatch(const int32_t* idx, const void* x, int64_t T, int64_t dim,
+                             int n_experts, int k, int32_t* counts, int32_t* offsets,
+                             int32_t* perm, int32_t* pos_of_slot, void* x_perm, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  if (T < 0 || dim <= 0) return FMOE_ERR_INVALID_ARG;
+  if (n_experts <= 0 || n_experts > FMOE_MAX_EXPERTS) return FMOE_ERR_TOO_MANY_EXPERTS;
+  if (k <= 0 || k > FMOE_MAX_TOPK || k > n_experts || dim % 64 != 0) return FMOE_ERR_SHAPE;
+  if (!counts || !offsets) return FMOE_ERR_INVALID_ARG;
+  const int64_t n_slots = T * k;
+  if (n_slots > INT32_MAX / 2) return FMOE_ERR_SHAPE;
+  hipStream_t s = as_stream(stream);
+  const int64_t nblocks = ceil_div(n_slots, kSlotsPerBlock);
+  if (T == 0) {
+    // Empty batch: every count and offset is zero (scan over zero blocks).
+    dispatch_scan_kernel<<<1, 64, 0, s>>>(nullptr, 0, n_experts, nullptr, counts, offsets);
+    return launch_status();
+  }
+  if (!idx || !x || !perm || !pos_of_slot || !workspace) return FMOE_ERR_INVALID_ARG;
+  if (workspace_bytes < fmoe_dispatch_workspace_bytes(T, n_experts, k)) return FMOE_ERR_WORKSPACE;
+  if (!aligned16(x) || (x_perm && !aligned16(x_perm))) return FMOE_ERR_ALIGN;
+  int32_t* block_hist = static_cast<int32_t*>(workspace);
+  int32_t* block_base = block_hist + nblocks * n_experts;
+  dispatch_hist_kernel<<<dim3(nblocks), dim3(kDispThreads), 0, s>>>(idx, (int)n_slots, n_experts,
+                                                                   block_hist);
+  dispatch_scan_kernel<<<1, 64, 0, s>>>(block_hist, (int)nblocks, n_experts, block_base, counts,
+                                        offsets);
+  dispatch_scatter_kernel<<<dim3(nblocks), dim3(kDispThreads), 0, s>>>(
+      idx, (int)n_slots, n_experts, block_base, perm, pos_of_slot);
+  if (x_perm) {
+    const int chunks = static_cast<int>(dim / 8);
+    const int64_t total = n_slots * chunks;
+    dispatch_gather_kernel<<<dim3(ceil_div(total, 256)), dim3(256), 0, s>>>(
+        perm, static_cast<const uint4*>(x), n_slots, chunks, k, static_cast<uint4*>(x_perm));
+  }
+  return launch_status();
+}

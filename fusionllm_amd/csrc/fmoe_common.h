@@ -1,0 +1,105 @@
+// fmoe_common.h — helpers shared by the gfx950 kernels of libfusionmoe.so.
+//
+// The whole library is compiled with -ffp-contract=off: every fused
+// multiply-add in the kernels is an explicit fmaf(), so that the rounding
+// steps are the ones written here (the router and the combine are
+// reproduced bit-for-bit by the CPU oracle).  MFMA instructions are not
+// affected by the flag.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/fusionmoe.h"
+
+namespace fmoe {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ---- bf16 <-> fp32 ---------------------------------------------------------
+__device__ __forceinline__ float bf2f(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+// Round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950), the rounding torch
+// uses for .to(torch.bfloat16).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  __bf16 b = static_cast<__bf16>(f);
+  return __builtin_bit_cast(uint16_t, b);
+}
+__device__ __forceinline__ float bf_round(float f) { return bf2f(f2bf(f)); }
+
+// Unpack 8 bf16 held in a uint4 into floats.
+__device__ __forceinline__ void unpack8(const uint4& v, float* f) {
+  f[0] = __uint_as_float(v.x << 16); f[1] = __uint_as_float(v.x & 0xffff0000u);
+  f[2] = __uint_as_float(v.y << 16); f[3] = __uint_as_float(v.y & 0xffff0000u);
+  f[4] = __uint_as_float(v.z << 16); f[5] = __uint_as_float(v.z & 0xffff0000u);
+  f[6] = __uint_as_float(v.w << 16); f[7] = __uint_as_float(v.w & 0xffff0000u);
+}
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
+}
+__device__ __forceinline__ uint4 pack8(const float* f) {
+  uint4 v;
+  v.x = pack2(f[0], f[1]); v.y = pack2(f[2], f[3]);
+  v.z = pack2(f[4], f[5]); v.w = pack2(f[6], f[7]);
+  return v;
+}
+
+// ---- exp and sigmoid for the router ----------------------------------------
+// e^x by Cody-Waite range reduction x = n*ln2 + r (|r| <= ln2/2) and the
+// degree-7 Taylor polynomial of e^r (truncation error < 6e-9 relative), then
+// an exact scaling by 2^n done in two halves so that denormal results are
+// formed correctly.  Written with explicit fmaf so the CPU oracle
+// (oracle/router_ref.c) evaluates the identical sequence.
+__host__ __device__ __forceinline__ float fm_pow2i(int n) {  // 2^n, -126 <= n <= 127
+  return __uint_as_float(static_cast<uint32_t>(n + 127) << 23);
+}
+__device__ __forceinline__ float fm_expf(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return __uint_as_float(0x7f800000u);
+  if (x < -103.97208404541016f) return 0.0f;
+  const float n = rintf(x * 1.4426950216293335f);
+  float r = fmaf(n, -0.693145751953125f, x);
+  r = fmaf(n, -1.4286067653302598e-06f, r);
+  float p = 1.0f / 5040.0f;
+  p = fmaf(p, r, 1.0f / 720.0f);
+  p = fmaf(p, r, 1.0f / 120.0f);
+  p = fmaf(p, r, 1.0f / 24.0f);
+  p = fmaf(p, r, 1.0f / 6.0f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int ni = static_cast<int>(n);
+  const int n1 = ni / 2;
+  const int n2 = ni - n1;
+  return (p * fm_pow2i(n1)) * fm_pow2i(n2);
+}
+__device__ __forceinline__ float fm_sigmoid(float l) { return 1.0f / (1.0f + fm_expf(-l)); }
+
+// Fast sigmoid for the SwiGLU epilogues (the result is rounded to bf16, so a
+// few fp32 ulps do not matter): v_exp_f32 computes 2^x.
+__device__ __forceinline__ float fast_sigmoid(float a) {
+  return 1.0f / (1.0f + __builtin_amdgcn_exp2f(-a * 1.4426950408889634f));
+}
+
+// Top-k order: a beats b if a is NaN and b is not, or a > b.  Scanning experts
+// in ascending order and replacing only on a strict win keeps ties on the
+// lowest index.
+__device__ __forceinline__ bool score_beats(float a, float b) {
+  const bool an = a != a, bn = b != b;
+  if (an || bn) return an && !bn;
+  return a > b;
+}
+
+// ---- status helpers (host) --------------------------------------------------
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FMOE_OK : FMOE_ERR_LAUNCH;
+}
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace fmoe

@@ -1,0 +1,718 @@
+// gemm.hip — grouped bf16 GEMMs on CDNA4 matrix cores (v_mfma_f32_32x32x16_bf16)
+// for the expert SwiGLU products of FusionLLM's DeepSeekMoE.
+//
+// Replaces SwiGLUExpert.forward (models/moe.py:20-21) called once per active
+// expert in the loop of moe.py:66-76 and once for the shared expert
+// (moe.py:86), and the autograd of those calls.  All experts (and the shared
+// expert as one more group) go into a single launch per product; the tile ->
+// (expert, rows) mapping is computed on the device from offsets[], so no
+// host synchronisation is needed for the ragged, skewed expert sizes.
+//
+// Tiling.  A workgroup computes a BM x BN tile of C with fp32 accumulators,
+// stepping K by 64.  Both operands are staged in LDS as "rows x 64" tiles,
+// K-contiguous (128 bytes per row), double buffered; the 16-byte chunks of a
+// row are XOR-swizzled so that the MFMA fragment reads (32 rows, one chunk)
+// and the transposing stores are free of bank conflicts.  An operand that is
+// MN-contiguous in memory (the weights in the dX products, both operands of
+// the weight gradients) is loaded as 8x8 blocks, transposed in registers and
+// stored K-contiguous.  Each wave owns a WTM x WTN sub-tile made of 32x32
+// MFMA blocks; fragment layout of v_mfma_f32_32x32x16_bf16: lane l supplies
+// A[l%32][8*(l/32) .. +7] and B[8*(l/32) .. +7][l%32] and receives
+// C[8*(r/4) + 4*(l/32) + r%4][l%32] in accumulator r.
+#include "fmoe_common.h"
+
+namespace fmoe {
+
+constexpr int kBK = 64;
+
+__device__ __forceinline__ uint32_t lds_off(int row, int chunk) {
+  return static_cast<uint32_t>(row) * 128u +
+         (static_cast<uint32_t>(chunk ^ ((row ^ (row >> 3)) & 7)) << 4);
+}
+
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_>
+struct Cfg {
+  static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+  static constexpr int NT = WAVES_M * WAVES_N * 64;
+  static constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+  static constexpr int FM = WTM / 32, FN = WTN / 32;
+  static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be made of 32x32 blocks");
+};
+
+// ---- operand staging --------------------------------------------------------
+// K-contiguous operand: ROWS rows x 64 k.  Thread t moves chunk t%8 of rows
+// t/8, t/8 + NT/8, ...
+template <int ROWS, int NT>
+struct KLoad {
+  static constexpr int PER = ROWS * 8 / NT;
+  static_assert(PER >= 1 && (ROWS * 8) % NT == 0, "K-major tile does not split evenly");
+  const uint16_t* src[PER];
+  uint4 reg[PER];
+  __device__ __forceinline__ static int row_of(int tid, int i) { return (tid >> 3) + i * (NT / 8); }
+  __device__ __forceinline__ static int chunk_of(int tid) { return tid & 7; }
+  __device__ __forceinline__ void load(int k0) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) reg[i] = *reinterpret_cast<const uint4*>(src[i] + k0);
+  }
+  __device__ __forceinline__ void store(uint8_t* s, int tid) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      *reinterpret_cast<uint4*>(s + lds_off(row_of(tid, i), chunk_of(tid))) = reg[i];
+  }
+};
+
+// MN-contiguous operand: memory is [k][mn]; the tile is ROWS mn x 64 k.  Work
+// item b = (mn block mb = b % (ROWS/8), k block kb = b / (ROWS/8)) moves an
+// 8 (k) x 8 (mn) block: 8 row loads of 16 bytes, an in-register transpose,
+// 8 stores of 16 bytes into LDS rows mb*8 .. mb*8+7 at chunk kb.  NTL threads
+// take part, numbered by the caller (ltid outside [0, NTL) does nothing), so
+// that two operands can be split over the two halves of a workgroup.
+template <int ROWS, int NTL>
+struct MNLoad {
+  static constexpr int NBLK = ROWS;  // (ROWS / 8) * (64 / 8)
+  static constexpr int PER = NBLK / NTL;
+  static_assert(NBLK % NTL == 0 && PER >= 1, "MN-major tile split");
+  uint4 reg[PER][8];
+  __device__ __forceinline__ static bool active(int ltid) { return ltid >= 0 && ltid < NTL; }
+  __device__ __forceinline__ static int blk(int ltid, int p) { return ltid + p * NTL; }
+  __device__ __forceinline__ static int mb_of(int b) { return b % (ROWS / 8); }
+  __device__ __forceinline__ static int kb_of(int b) { return b / (ROWS / 8); }
+
+  // rowptr(k) -> pointer to element (k, 0) of the operand, nullptr for a row
+  // that lies outside the reduction range (loaded as zeros).  Columns are
+  // clamped to [0, mn_limit - 8]: a clamped block only feeds outputs that the
+  // epilogue does not store.
+  template <class RowPtr>
+  __device__ __forceinline__ void load(int ltid, int k0, int mn0, int mn_limit, RowPtr rowptr) {
+    if (!active(ltid)) return;
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int b = blk(ltid, p);
+      int col = mn0 + mb_of(b) * 8;
+      col = col < mn_limit - 8 ? col : mn_limit - 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint16_t* r = rowptr(k0 + kb_of(b) * 8 + i);
+        if (r) reg[p][i] = *reinterpret_cast<const uint4*>(r + col);
+        else reg[p][i] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(uint8_t* s, int ltid) const {
+    if (!active(ltid)) return;
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int b = blk(ltid, p);
+      const uint32_t* in = reinterpret_cast<const uint32_t*>(&reg[p][0]);  // in[4*i + dword]
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t lo = in[4 * (2 * q) + (j >> 1)];
+          const uint32_t hi = in[4 * (2 * q + 1) + (j >> 1)];
+          o[q] = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+        }
+        *reinterpret_cast<uint4*>(s + lds_off(mb_of(b) * 8 + j, kb_of(b))) =
+            make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  }
+};
+
+// One K-tile (64) of MFMAs from the staged A and B tiles.
+template <class C>
+__device__ __forceinline__ void mma_ktile(const uint8_t* sA, const uint8_t* sB,
+                                          f32x16 (&acc)[C::FM][C::FN], int wm, int wn, int lane) {
+#pragma unroll
+  for (int kk = 0; kk < kBK / 16; ++kk) {
+    const int chunk = kk * 2 + (lane >> 5);
+    bf16x8 a[C::FM], b[C::FN];
+#pragma unroll
+    for (int fm = 0; fm < C::FM; ++fm)
+      a[fm] = *reinterpret_cast<const bf16x8*>(sA + lds_off(wm * C::WTM + fm * 32 + (lane & 31), chunk));
+#pragma unroll
+    for (int fn = 0; fn < C::FN; ++fn)
+      b[fn] = *reinterpret_cast<const bf16x8*>(sB + lds_off(wn * C::WTN + fn * 32 + (lane & 31), chunk));
+#pragma unroll
+    for (int fm = 0; fm < C::FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < C::FN; ++fn)
+        acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[fm], b[fn], acc[fm][fn], 0, 0, 0);
+  }
+}
+
+// ---- row-grouped products ---------------------------------------------------
+enum GemmMode { GATEUP_FWD = 0, DOWN_FWD = 1, DOWN_BWD = 2, GATEUP_BWD = 3 };
+
+struct GemmArgs {
+  const uint16_t* a_routed;  // [rows_routed, K]
+  const uint16_t* a_shared;  // [rows_shared, K] (nullptr: rows follow the routed rows)
+  int64_t lda;
+  const int32_t* offsets;  // [E+1], device
+  int E;
+  int rows_routed;
+  int rows_shared;
+  int K;        // reduction length
+  int N;        // output columns (GATEUP_FWD: inter = h columns)
+  int inter;    // SwiGLU width (GATEUP_FWD, DOWN_BWD, GATEUP_BWD)
+  int64_t ldb;  // leading dimension of the weights
+  uint16_t* c0;  // main output (ab / out / d_ab / dx_rows)
+  uint16_t* c1;  // GATEUP_FWD: h
+  const uint16_t* aux;  // DOWN_BWD: ab
+  int64_t ldc0, ldc1, ldaux;
+  const uint16_t* b0[FMOE_MAX_EXPERTS + 1];  // w1 / w2 / w2 / w1
+  const uint16_t* b1[FMOE_MAX_EXPERTS + 1];  // w3 / - / - / w3
+};
+
+template <class C, int MODE>
+__global__ __launch_bounds__(C::NT) void grouped_gemm_kernel(const GemmArgs args) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::STAGE_BYTES];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+
+  // Columns covered by one tile: GATEUP_FWD interleaves w1 and w3 rows, so a
+  // tile of BN accumulator columns covers BN/2 columns of h.
+  constexpr int TN_COLS = (MODE == GATEUP_FWD) ? C::BN / 2 : C::BN;
+  const int tiles_n = (args.N + TN_COLS - 1) / TN_COLS;
+
+  // ---- tile -> (group, m tile, n tile)
+  const int G = args.E + (args.rows_shared > 0 ? 1 : 0);
+  int tile = blockIdx.x;
+  int g = 0, M = 0, row_base = 0;
+  for (; g < G; ++g) {
+    if (g < args.E) {
+      row_base = args.offsets[g];
+      M = args.offsets[g + 1] - row_base;
+    } else {
+      row_base = args.rows_routed;
+      M = args.rows_shared;
+    }
+    const int nt = ((M + C::BM - 1) / C::BM) * tiles_n;
+    if (tile < nt) break;
+    tile -= nt;
+  }
+  if (g >= G) return;  // grid is an upper bound on the tile count
+  const int tm = tile / tiles_n, tn = tile % tiles_n;
+  const int m0 = tm * C::BM;
+  const int n0 = tn * TN_COLS;
+
+  const uint16_t* A = (g < args.E || args.a_shared == nullptr)
+                          ? args.a_routed + static_cast<int64_t>(row_base) * args.lda
+                          : args.a_shared;
+
+  // ---- operand loaders
+  KLoad<C::BM, C::NT> la;
+#pragma unroll
+  for (int i = 0; i < la.PER; ++i) {
+    int r = m0 + KLoad<C::BM, C::NT>::row_of(tid, i);
+    r = r < M ? r : M - 1;
+    la.src[i] = A + static_cast<int64_t>(r) * args.lda + KLoad<C::BM, C::NT>::chunk_of(tid) * 8;
+  }
+  constexpr bool B_KMAJOR = (MODE == GATEUP_FWD || MODE == DOWN_FWD);
+  KLoad<C::BN, C::NT> lbk;
+  constexpr int B_NTL = C::NT < C::BN ? C::NT : C::BN;
+  MNLoad<C::BN, B_NTL> lbm;
+  const int b_ltid = tid - (C::NT - B_NTL);
+  const uint16_t* W0 = args.b0[g];
+  const uint16_t* W1 = args.b1[g];
+  if constexpr (B_KMAJOR) {
+#pragma unroll
+    for (int i = 0; i < lbk.PER; ++i) {
+      const int r = KLoad<C::BN, C::NT>::row_of(tid, i);
+      const uint16_t* base;
+      int n;
+      if constexpr (MODE == GATEUP_FWD) {
+        // accumulator column block fn of wave column wb: even fn -> w1, odd -> w3,
+        // both for h columns n0 + wb*WTN/2 + (fn/2)*32 + i.
+        const int wb = r / C::WTN, within = r % C::WTN, fn = within / 32;
+        n = n0 + wb * (C::WTN / 2) + (fn / 2) * 32 + (within % 32);
+        base = (fn & 1) ? W1 : W0;
+      } else {
+        n = n0 + r;
+        base = W0;
+      }
+      n = n < args.N ? n : args.N - 1;
+      lbk.src[i] = base + static_cast<int64_t>(n) * args.ldb + KLoad<C::BN, C::NT>::chunk_of(tid) * 8;
+    }
+  }
+  auto b_rowptr = [&](int k) -> const uint16_t* {
+    if constexpr (MODE == GATEUP_BWD) {
+      // K runs over [w1 rows | w3 rows] (2*inter), each row of length N = dim.
+      return k < args.inter ? W0 + static_cast<int64_t>(k) * args.ldb
+                            : W1 + static_cast<int64_t>(k - args.inter) * args.ldb;
+    } else {
+      return W0 + static_cast<int64_t>(k) * args.ldb;
+    }
+  };
+
+  auto load_tile = [&](int k0) {
+    la.load(k0);
+    if constexpr (B_KMAJOR) lbk.load(k0);
+    else lbm.load(b_ltid, k0, n0, args.N, b_rowptr);
+  };
+  auto store_tile = [&](int buf) {
+    uint8_t* sA = smem + buf * C::STAGE_BYTES;
+    la.store(sA, tid);
+    if constexpr (B_KMAJOR) lbk.store(sA + C::A_BYTES, tid);
+    else lbm.store(sA + C::A_BYTES, b_ltid);
+  };
+
+  f32x16 acc[C::FM][C::FN];
+#pragma unroll
+  for (int fm = 0; fm < C::FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < C::FN; ++fn)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
+
+  const int nk = args.K / kBK;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) load_tile((kt + 1) * kBK);
+    const uint8_t* sA = smem + buf * C::STAGE_BYTES;
+    mma_ktile<C>(sA, sA + C::A_BYTES, acc, wm, wn, lane);
+    if (kt + 1 < nk) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue
+  const int row_l = (lane >> 5) * 4;
+  if constexpr (MODE == GATEUP_FWD) {
+#pragma unroll
+    for (int fm = 0; fm < C::FM; ++fm) {
+#pragma unroll
+      for (int p = 0; p < C::FN / 2; ++p) {
+        const int col = n0 + wn * (C::WTN / 2) + p * 32 + (lane & 31);
+        if (col >= args.N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * C::WTM + fm * 32 + (r >> 2) * 8 + row_l + (r & 3);
+          if (m >= M) continue;
+          const float a = bf_round(acc[fm][2 * p][r]);
+          const float b = bf_round(acc[fm][2 * p + 1][r]);
+          const float s = bf_round(a * fast_sigmoid(a));
+          const int64_t row = row_base + m;
+          args.c0[row * args.ldc0 + col] = f2bf(a);
+          args.c0[row * args.ldc0 + args.inter + col] = f2bf(b);
+          args.c1[row * args.ldc1 + col] = f2bf(s * b);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int fm = 0; fm < C::FM; ++fm) {
+#pragma unroll
+      for (int fn = 0; fn < C::FN; ++fn) {
+        const int col = n0 + wn * C::WTN + fn * 32 + (lane & 31);
+        if (col >= args.N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * C::WTM + fm * 32 + (r >> 2) * 8 + row_l + (r & 3);
+          if (m >= M) continue;
+          const int64_t row = row_base + m;
+          if constexpr (MODE == DOWN_BWD) {
+            // h = s * b with s = bf16(silu(a)); dh arrives bf16-rounded.
+            const float dh = bf_round(acc[fm][fn][r]);
+            const float a = bf2f(args.aux[row * args.ldaux + col]);
+            const float b = bf2f(args.aux[row * args.ldaux + args.inter + col]);
+            const float sg = fast_sigmoid(a);
+            const float s = bf_round(a * sg);
+            const float ds = bf_round(dh * b);
+            const float da = ds * (sg * (1.0f + a * (1.0f - sg)));
+            args.c0[row * args.ldc0 + col] = f2bf(da);
+            args.c0[row * args.ldc0 + args.inter + col] = f2bf(dh * s);
+          } else {
+            args.c0[row * args.ldc0 + col] = f2bf(acc[fm][fn][r]);
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---- weight gradients (K-grouped) -------------------------------------------
+// G_e = A_e^T B_e with A_e [M_e, m_out], B_e [M_e, n_out] (both MN-contiguous).
+// Work unit = (group, K chunk of kc rows, output tile).  A group whose rows fit
+// in one chunk writes its tile directly; otherwise every chunk writes an fp32
+// partial and wgrad_reduce_kernel adds the chunks of a group in chunk order.
+struct WgradArgs {
+  const uint16_t* a_routed;
+  const uint16_t* a_shared;
+  int64_t lda;
+  const uint16_t* b_routed;
+  const uint16_t* b_shared;
+  int64_t ldb;
+  const int32_t* offsets;
+  int E;
+  int rows_routed;
+  int rows_shared;
+  int m_out, n_out, m_split;
+  int kc;
+  int out_dtype;
+  float* partial;
+  void* out_lo[FMOE_MAX_EXPERTS + 1];
+  void* out_hi[FMOE_MAX_EXPERTS + 1];
+};
+
+__device__ __forceinline__ void group_rows(const WgradArgs& a, int g, int& row_base, int& M) {
+  if (g < a.E) {
+    row_base = a.offsets[g];
+    M = a.offsets[g + 1] - row_base;
+  } else {
+    row_base = a.rows_routed;
+    M = a.rows_shared;
+  }
+}
+
+__device__ __forceinline__ void store_grad(const WgradArgs& a, int g, int m, int n, float v) {
+  const int64_t o = (m < a.m_split) ? static_cast<int64_t>(m) * a.n_out + n
+                                    : static_cast<int64_t>(m - a.m_split) * a.n_out + n;
+  void* base = (m < a.m_split) ? a.out_lo[g] : a.out_hi[g];
+  if (a.out_dtype == FMOE_BF16) static_cast<uint16_t*>(base)[o] = f2bf(v);
+  else static_cast<float*>(base)[o] = v;
+}
+
+template <class C>
+__global__ __launch_bounds__(C::NT) void wgrad_kernel(const WgradArgs args) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::STAGE_BYTES];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+  const int tiles_m = (args.m_out + C::BM - 1) / C::BM;
+  const int tiles_n = (args.n_out + C::BN - 1) / C::BN;
+  const int tiles = tiles_m * tiles_n;
+  const int G = args.E + (args.rows_shared > 0 ? 1 : 0);
+
+  int unit = blockIdx.x;
+  int g = 0, row_base = 0, M = 0, chunks = 0, pbase = 0;
+  for (; g < G; ++g) {
+    group_rows(args, g, row_base, M);
+    chunks = (M + args.kc - 1) / args.kc;
+    const int nu = chunks * tiles;
+    if (unit < nu) break;
+    unit -= nu;
+    if (chunks > 1) pbase += chunks;
+  }
+  if (g >= G) return;
+  const int chunk = unit / tiles, tile = unit % tiles;
+  const int tm = tile / tiles_n, tn = tile % tiles_n;
+  const int m0 = tm * C::BM, n0 = tn * C::BN;
+  const int k_begin = chunk * args.kc;
+  const int k_end = min(M, k_begin + args.kc);
+
+  const bool shared_sep = (g >= args.E);
+  const uint16_t* A = (shared_sep && args.a_shared) ? args.a_shared
+                                                   : args.a_routed + static_cast<int64_t>(row_base) * args.lda;
+  const uint16_t* B = (shared_sep && args.b_shared) ? args.b_shared
+                                                   : args.b_routed + static_cast<int64_t>(row_base) * args.ldb;
+  auto a_row = [&](int k) -> const uint16_t* {
+    return k < k_end ? A + static_cast<int64_t>(k) * args.lda : nullptr;
+  };
+  auto b_row = [&](int k) -> const uint16_t* {
+    return k < k_end ? B + static_cast<int64_t>(k) * args.ldb : nullptr;
+  };
+  // With 512 threads the A blocks go to threads 0-255 and the B blocks to
+  // threads 256-511; with 256 threads every thread moves one block of each.
+  constexpr int NTL = C::NT >= 512 ? C::NT / 2 : C::NT;
+  MNLoad<C::BM, NTL> la;
+  MNLoad<C::BN, NTL> lb;
+  const int a_ltid = tid;
+  const int b_ltid = C::NT >= 512 ? tid - NTL : tid;
+  auto load_tile = [&](int k0) {
+    la.load(a_ltid, k0, m0, args.m_out, a_row);
+    lb.load(b_ltid, k0, n0, args.n_out, b_row);
+  };
+  auto store_tile = [&](int buf) {
+    uint8_t* sA = smem + buf * C::STAGE_BYTES;
+    la.store(sA, a_ltid);
+    lb.store(sA + C::A_BYTES, b_ltid);
+  };
+
+  f32x16 acc[C::FM][C::FN];
+#pragma unroll
+  for (int fm = 0; fm < C::FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < C::FN; ++fn)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
+
+  const int nk = (k_end - k_begin + kBK - 1) / kBK;
+  load_tile(k_begin);
+  store_tile(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) load_tile(k_begin + (kt + 1) * kBK);
+    const uint8_t* sA = smem + buf * C::STAGE_BYTES;
+    mma_ktile<C>(sA, sA + C::A_BYTES, acc, wm, wn, lane);
+    if (kt + 1 < nk) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  const int row_l = (lane >> 5) * 4;
+  const int64_t mn = static_cast<int64_t>(args.m_out) * args.n_out;
+  float* part = (chunks > 1) ? args.partial + static_cast<int64_t>(pbase + chunk) * mn : nullptr;
+#pragma unroll
+  for (int fm = 0; fm < C::FM; ++fm) {
+#pragma unroll
+    for (int fn = 0; fn < C::FN; ++fn) {
+      const int n = n0 + wn * C::WTN + fn * 32 + (lane & 31);
+      if (n >= args.n_out) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * C::WTM + fm * 32 + (r >> 2) * 8 + row_l + (r & 3);
+        if (m >= args.m_out) continue;
+        if (part) part[static_cast<int64_t>(m) * args.n_out + n] = acc[fm][fn][r];
+        else store_grad(args, g, m, n, acc[fm][fn][r]);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void wgrad_reduce_kernel(const WgradArgs args) {
+  const int g = blockIdx.y;
+  int row_base, M;
+  group_rows(args, g, row_base, M);
+  const int chunks = (M + args.kc - 1) / args.kc;
+  if (chunks <= 1) return;
+  int pbase = 0;
+  for (int q = 0; q < g; ++q) {
+    int rb, Mq;
+    group_rows(args, q, rb, Mq);
+    const int cq = (Mq + args.kc - 1) / args.kc;
+    if (cq > 1) pbase += cq;
+  }
+  const int64_t mn = static_cast<int64_t>(args.m_out) * args.n_out;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= mn) return;
+  float acc = 0.0f;
+  for (int c = 0; c < chunks; ++c) acc = acc + args.partial[(pbase + c) * mn + i];
+  const int m = static_cast<int>(i / args.n_out), n = static_cast<int>(i % args.n_out);
+  store_grad(args, g, m, n, acc);
+}
+
+// ---- host side --------------------------------------------------------------
+using CfgRow = Cfg<256, 256, 2, 4>;    // 512 threads, wave tile 128 x 64
+using CfgWgrad = Cfg<256, 256, 2, 4>;
+
+int check_common(int n_experts, int64_t rows_routed, int64_t rows_shared, int64_t dim, int64_t inter) {
+  if (n_experts <= 0 || n_experts > FMOE_MAX_EXPERTS) return FMOE_ERR_TOO_MANY_EXPERTS;
+  if (rows_routed < 0 || rows_shared < 0 || dim <= 0 || inter <= 0) return FMOE_ERR_INVALID_ARG;
+  if (dim % 64 != 0 || inter % 64 != 0) return FMOE_ERR_SHAPE;
+  if (rows_routed + rows_shared > INT32_MAX / 2) return FMOE_ERR_SHAPE;
+  return FMOE_OK;
+}
+
+template <class C, int MODE>
+int launch_rows(GemmArgs& a, int64_t rows_routed, int64_t rows_shared, int E, void* stream) {
+  constexpr int TN_COLS = (MODE == GATEUP_FWD) ? C::BN / 2 : C::BN;
+  const int64_t tiles_n = ceil_div(a.N, TN_COLS);
+  // Upper bound of sum over groups of ceil(M_g / BM): floor(rows/BM) + groups.
+  const int64_t mt = rows_routed / C::BM + E + ceil_div(rows_shared, C::BM);
+  const int64_t grid = mt * tiles_n;
+  if (grid <= 0) return FMOE_OK;
+  grouped_gemm_kernel<C, MODE><<<dim3(grid), dim3(C::NT), 0, as_stream(stream)>>>(a);
+  return launch_status();
+}
+
+void fill_groups(GemmArgs& a, const int32_t* offsets, int E, int64_t rows_routed, int64_t rows_shared) {
+  a.offsets = offsets;
+  a.E = E;
+  a.rows_routed = static_cast<int>(rows_routed);
+  a.rows_shared = static_cast<int>(rows_shared);
+}
+
+}  // namespace fmoe
+
+using namespace fmoe;
+
+extern "C" int fmoe_gateup_fwd(const void* x_routed, const void* x_shared, const int32_t* offsets,
+                               int n_experts, int64_t rows_routed, int64_t rows_shared, int64_t dim,
+                               int64_t inter, const void* const* w1, const void* const* w3,
+                               void* ab, void* h, void* stream) {
+  int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
+  if (st) return st;
+  if (rows_routed + rows_shared == 0) return FMOE_OK;
+  if (!offsets || !w1 || !w3 || !ab || !h || (rows_routed && !x_routed) ||
+      (rows_shared && !x_shared))
+    return FMOE_ERR_INVALID_ARG;
+  GemmArgs a = {};
+  a.a_routed = static_cast<const uint16_t*>(x_routed);
+  a.a_shared = static_cast<const uint16_t*>(x_shared);
+  a.lda = dim;
+  fill_groups(a, offsets, n_experts, rows_routed, rows_shared);
+  a.K = static_cast<int>(dim);
+  a.N = static_cast<int>(inter);
+  a.inter = static_cast<int>(inter);
+  a.ldb = dim;
+  a.c0 = static_cast<uint16_t*>(ab);
+  a.c1 = static_cast<uint16_t*>(h);
+  a.ldc0 = 2 * inter;
+  a.ldc1 = inter;
+  const int G = n_experts + (rows_shared > 0 ? 1 : 0);
+  for (int g = 0; g < G; ++g) {
+    if (!w1[g] || !w3[g]) return FMOE_ERR_INVALID_ARG;
+    a.b0[g] = static_cast<const uint16_t*>(w1[g]);
+    a.b1[g] = static_cast<const uint16_t*>(w3[g]);
+  }
+  return launch_rows<CfgRow, GATEUP_FWD>(a, rows_routed, rows_shared, n_experts, stream);
+}
+
+extern "C" int fmoe_down_fwd(const void* h, const int32_t* offsets, int n_experts,
+                             int64_t rows_routed, int64_t rows_shared, int64_t dim, int64_t inter,
+                             const void* const* w2, void* out, void* stream) {
+  int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
+  if (st) return st;
+  if (rows_routed + rows_shared == 0) return FMOE_OK;
+  if (!h || !offsets || !w2 || !out) return FMOE_ERR_INVALID_ARG;
+  GemmArgs a = {};
+  a.a_routed = static_cast<const uint16_t*>(h);
+  a.a_shared = nullptr;
+  a.lda = inter;
+  fill_groups(a, offsets, n_experts, rows_routed, rows_shared);
+  a.K = static_cast<int>(inter);
+  a.N = static_cast<int>(dim);
+  a.inter = static_cast<int>(inter);
+  a.ldb = inter;
+  a.c0 = static_cast<uint16_t*>(out);
+  a.ldc0 = dim;
+  const int G = n_experts + (rows_shared > 0 ? 1 : 0);
+  for (int g = 0; g < G; ++g) {
+    if (!w2[g]) return FMOE_ERR_INVALID_ARG;
+    a.b0[g] = static_cast<const uint16_t*>(w2[g]);
+  }
+  return launch_rows<CfgRow, DOWN_FWD>(a, rows_routed, rows_shared, n_experts, stream);
+}
+
+extern "C" int fmoe_down_bwd_dx(const void* d_out_routed, const void* d_out_shared,
+                                const int32_t* offsets, int n_experts, int64_t rows_routed,
+                                int64_t rows_shared, int64_t dim, int64_t inter,
+                                const void* const* w2, const void* ab, void* d_ab, void* stream) {
+  int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
+  if (st) return st;
+  if (rows_routed + rows_shared == 0) return FMOE_OK;
+  if (!offsets || !w2 || !ab || !d_ab || (rows_routed && !d_out_routed) ||
+      (rows_shared && !d_out_shared))
+    return FMOE_ERR_INVALID_ARG;
+  GemmArgs a = {};
+  a.a_routed = static_cast<const uint16_t*>(d_out_routed);
+  a.a_shared = static_cast<const uint16_t*>(d_out_shared);
+  a.lda = dim;
+  fill_groups(a, offsets, n_experts, rows_routed, rows_shared);
+  a.K = static_cast<int>(dim);
+  a.N = static_cast<int>(inter);
+  a.inter = static_cast<int>(inter);
+  a.ldb = inter;  // w2 is [dim, inter]: row k = dim index, columns = inter
+  a.c0 = static_cast<uint16_t*>(d_ab);
+  a.ldc0 = 2 * inter;
+  a.aux = static_cast<const uint16_t*>(ab);
+  a.ldaux = 2 * inter;
+  const int G = n_experts + (rows_shared > 0 ? 1 : 0);
+  for (int g = 0; g < G; ++g) {
+    if (!w2[g]) return FMOE_ERR_INVALID_ARG;
+    a.b0[g] = static_cast<const uint16_t*>(w2[g]);
+  }
+  return launch_rows<CfgRow, DOWN_BWD>(a, rows_routed, rows_shared, n_experts, stream);
+}
+
+extern "C" int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int n_experts,
+                                  int64_t rows_routed, int64_t rows_shared, int64_t dim,
+                                  int64_t inter, const void* const* w1, const void* const* w3,
+                                  void* dx_rows, void* stream) {
+  int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
+  if (st) return st;
+  if (rows_routed + rows_shared == 0) return FMOE_OK;
+  if (!d_ab || !offsets || !w1 || !w3 || !dx_rows) return FMOE_ERR_INVALID_ARG;
+  GemmArgs a = {};
+  a.a_routed = static_cast<const uint16_t*>(d_ab);
+  a.a_shared = nullptr;
+  a.lda = 2 * inter;
+  fill_groups(a, offsets, n_experts, rows_routed, rows_shared);
+  a.K = static_cast<int>(2 * inter);
+  a.N = static_cast<int>(dim);
+  a.inter = static_cast<int>(inter);
+  a.ldb = dim;  // w1, w3 are [inter, dim]: row k = inter index, columns = dim
+  a.c0 = static_cast<uint16_t*>(dx_rows);
+  a.ldc0 = dim;
+  const int G = n_experts + (rows_shared > 0 ? 1 : 0);
+  for (int g = 0; g < G; ++g) {
+    if (!w1[g] || !w3[g]) return FMOE_ERR_INVALID_ARG;
+    a.b0[g] = static_cast<const uint16_t*>(w1[g]);
+    a.b1[g] = static_cast<const uint16_t*>(w3[g]);
+  }
+  return launch_rows<CfgRow, GATEUP_BWD>(a, rows_routed, rows_shared, n_experts, stream);
+}
+
+namespace fmoe {
+// Rows per K chunk of the weight gradient: a multiple of 64 chosen so that the
+// largest possible group (all rows) splits into about 4 chunks.
+int64_t wgrad_kc(int64_t rows_routed, int64_t rows_shared) {
+  const int64_t rows = rows_routed > rows_shared ? rows_routed : rows_shared;
+  int64_t kc = ceil_div(ceil_div(rows, 4), 64) * 64;
+  return kc < 1024 ? 1024 : kc;
+}
+}  // namespace fmoe
+
+extern "C" size_t fmoe_weight_grad_workspace_bytes(int64_t rows_routed, int64_t rows_shared,
+                                                   int n_experts, int64_t m_out, int64_t n_out) {
+  if (rows_routed < 0 || rows_shared < 0 || n_experts <= 0 || m_out <= 0 || n_out <= 0) return 0;
+  const int64_t kc = wgrad_kc(rows_routed, rows_shared);
+  // sum over groups of ceil(M_g / kc) <= floor(rows / kc) + groups
+  const int64_t chunks = (rows_routed + rows_shared) / kc + n_experts + 1;
+  return static_cast<size_t>(chunks * m_out * n_out) * sizeof(float);
+}
+
+extern "C" int fmoe_weight_grad(const void* a_routed, const void* a_shared, int64_t lda,
+                                const void* b_routed, const void* b_shared, int64_t ldb,
+                                const int32_t* offsets, int n_experts, int64_t rows_routed,
+                                int64_t rows_shared, int64_t m_out, int64_t n_out, int64_t m_split,
+                                void* const* out_lo, void* const* out_hi, int out_dtype,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  int st = check_common(n_experts, rows_routed, rows_shared, m_out, n_out);
+  if (st) return st;
+  if (out_dtype != FMOE_BF16 && out_dtype != FMOE_F32) return FMOE_ERR_DTYPE;
+  if (m_split <= 0 || m_split > m_out) return FMOE_ERR_SHAPE;
+  if (rows_routed + rows_shared == 0) return FMOE_OK;
+  if (!offsets || !out_lo || (m_split < m_out && !out_hi) || (rows_routed && (!a_routed || !b_routed)))
+    return FMOE_ERR_INVALID_ARG;
+  if (lda % 8 != 0 || ldb % 8 != 0) return FMOE_ERR_ALIGN;
+  if (workspace_bytes < fmoe_weight_grad_workspace_bytes(rows_routed, rows_shared, n_experts, m_out, n_out))
+    return FMOE_ERR_WORKSPACE;
+  if (!workspace) return FMOE_ERR_INVALID_ARG;
+  WgradArgs a = {};
+  a.a_routed = static_cast<const uint16_t*>(a_routed);
+  a.a_shared = static_cast<const uint16_t*>(a_shared);
+  a.lda = lda;
+  a.b_routed = static_cast<const uint16_t*>(b_routed);
+  a.b_shared = static_cast<const uint16_t*>(b_shared);
+  a.ldb = ldb;
+  a.offsets = offsets;
+  a.E = n_experts;
+  a.rows_routed = static_cast<int>(rows_routed);
+  a.rows_shared = static_cast<int>(rows_shared);
+  a.m_out = static_cast<int>(m_out);
+  a.n_out = static_cast<int>(n_out);
+  a.m_split = static_cast<int>(m_split);
+  a.kc = static_cast<int>(wgrad_kc(rows_routed, rows_shared));
+  a.out_dtype = out_dtype;
+  a.partial = static_cast<float*>(workspace);
+  const int G = n_experts + (rows_shared > 0 ? 1 : 0);
+  for (int g = 0; g < G; ++g) {
+    if (!out_lo[g] || (m_split < m_out && !out_hi[g])) return FMOE_ERR_INVALID_ARG;
+    a.out_lo[g] = out_lo[g];
+    a.out_hi[g] = (m_split < m_out) ? out_hi[g] : nullptr;
+  }
+  using C = CfgWgrad;
+  const int64_t tiles = ceil_div(m_out, C::BM) * ceil_div(n_out, C::BN);
+  const int64_t max_chunks = (rows_routed + rows_shared) / a.kc + G;
+  hipStream_t s = as_stream(stream);
+  wgrad_kernel<C><<<dim3(max_chunks * tiles), dim3(C::NT), 0, s>>>(a);
+  const int64_t mn = m_out * n_out;
+  wgrad_reduce_kernel<<<dim3(ceil_div(mn, 256), G), dim3(256), 0, s>>>(a);
+  return launch_status();
+}

@@ -1,0 +1,273 @@
+// router.hip — biased-sigmoid top-k routing (forward) and its backward.
+//
+// Forward replaces DeepSeekMoE._route, FusionLLM models/moe.py:44-50.
+// Backward replaces the autograd of the same lines plus the gate Linear
+// weight/bias gradient.
+//
+// Logit summation order (reproduced exactly by oracle/router_ref.c):
+//   16 lanes cooperate on one token.  dim is cut into 8-element chunks;
+//   lane j owns chunks j, j+16, j+32, ... and accumulates, chunk by chunk and
+//   element by element in ascending order, acc = fmaf(x, w, acc) from 0.
+//   The 16 partials are then combined by an xor butterfly with offsets
+//   8, 4, 2, 1 (each stage: p[j] = p[j] + p[j^off]); finally logit = p + bias.
+//   Products of two bf16 values are exact in fp32, so fmaf and mul+add agree.
+#include "fmoe_common.h"
+
+namespace fmoe {
+
+constexpr int kRouterLanes = 16;
+
+template <int EB>
+__global__ __launch_bounds__(256) void router_fwd_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg,
+    const uint16_t* __restrict__ bg, int T, int dim, int E, int k, float route_scale,
+    int32_t* __restrict__ idx, int64_t* __restrict__ idx64, float* __restrict__ wout,
+    float* __restrict__ vout) {
+  const int lane16 = threadIdx.x % kRouterLanes;
+  const int t = (blockIdx.x * blockDim.x + threadIdx.x) / kRouterLanes;
+  const bool active = t < T;
+  const int tc = active ? t : T - 1;  // keep all lanes in the shuffles
+
+  float acc[EB];
+#pragma unroll
+  for (int e = 0; e < EB; ++e) acc[e] = 0.0f;
+
+  const int nchunk = dim / 8;
+  const uint4* xrow = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(tc) * dim);
+  for (int c = lane16; c < nchunk; c += kRouterLanes) {
+    float xf[8];
+    unpack8(xrow[c], xf);
+#pragma unroll
+    for (int e = 0; e < EB; ++e) {
+      if (e < E) {
+        const uint4 wv = reinterpret_cast<const uint4*>(wg + static_cast<int64_t>(e) * dim)[c];
+        float wf[8];
+        unpack8(wv, wf);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[e] = fmaf(xf[i], wf[i], acc[e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int off = kRouterLanes / 2; off >= 1; off >>= 1) {
+#pragma unroll
+    for (int e = 0; e < EB; ++e) acc[e] = acc[e] + __shfl_xor(acc[e], off, kRouterLanes);
+  }
+
+  // Every lane of the group now holds all logits; scores and top-k are
+  // computed redundantly and lane j < k writes the j-th choice.
+  float s[EB];
+#pragma unroll
+  for (int e = 0; e < EB; ++e) s[e] = (e < E) ? fm_sigmoid(acc[e] + bf2f(bg[e])) : 0.0f;
+
+  uint64_t taken = 0;
+  int sel[FMOE_MAX_TOPK];
+  float val[FMOE_MAX_TOPK];
+#pragma unroll
+  for (int j = 0; j < FMOE_MAX_TOPK; ++j) {
+    sel[j] = 0;
+    val[j] = 0.0f;
+    if (j < k) {
+      int best = -1;
+      float bv = 0.0f;
+#pragma unroll
+      for (int e = 0; e < EB; ++e) {
+        if (e < E && !((taken >> e) & 1ull)) {
+          if (best < 0 || score_beats(s[e], bv)) { best = e; bv = s[e]; }
+        }
+      }
+      taken |= 1ull << best;
+      sel[j] = best;
+      val[j] = bv;
+    }
+  }
+  float sum = val[0];
+#pragma unroll
+  for (int j = 1; j < FMOE_MAX_TOPK; ++j)
+    if (j < k) sum = sum + val[j];
+  const float denom = sum + 1e-10f;
+  if (active && lane16 < k) {
+    int e_sel = sel[0];
+    float v_sel = val[0];
+#pragma unroll
+    for (int q = 1; q < FMOE_MAX_TOPK; ++q)
+      if (q == lane16) { e_sel = sel[q]; v_sel = val[q]; }
+    const int64_t o = static_cast<int64_t>(t) * k + lane16;
+    idx[o] = e_sel;
+    if (idx64) idx64[o] = e_sel;
+    wout[o] = (v_sel / denom) * route_scale;
+    vout[o] = v_sel;
+  }
+}
+
+// ---- backward ----------------------------------------------------------------
+// Per token: w_j = (v_j / D) * rs with D = sum(v) + 1e-10.  Autograd of that:
+//   dq_j = dw_j * rs;  dv_j = dq_j / D + dS,  dS = -sum_j dq_j * v_j / D^2;
+// top-k backward routes dv_j to the selected score; sigmoid backward gives
+//   dlogit_j = dv_j * (1 - v_j) * v_j.
+__global__ __launch_bounds__(256) void router_dlogit_kernel(
+    const float* __restrict__ dw, const float* __restrict__ v, int T, int k, float rs,
+    float* __restrict__ dl) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= T) return;
+  const float* dwt = dw + static_cast<int64_t>(t) * k;
+  const float* vt = v + static_cast<int64_t>(t) * k;
+  float sum = vt[0];
+  for (int j = 1; j < k; ++j) sum = sum + vt[j];
+  const float D = sum + 1e-10f;
+  float dS = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    const float dq = dwt[j] * rs;
+    dS = dS - (dq * vt[j]) / (D * D);
+  }
+  for (int j = 0; j < k; ++j) {
+    const float dq = dwt[j] * rs;
+    const float dv = dq / D + dS;
+    dl[static_cast<int64_t>(t) * k + j] = (dv * (1.0f - vt[j])) * vt[j];
+  }
+}
+
+// Gate weight/bias gradient as a segmented column reduction over the
+// expert-contiguous rows:  dWg[e] = sum_{r in e} dl[perm[r]] * x_perm[r],
+// dbg[e] = sum_{r in e} dl[perm[r]].  Stage 1: each block reduces a chunk of
+// kChunkRows rows of one expert (chunk c of expert e covers rows
+// offsets[e] + c*kChunkRows ...) into partial[e][c][dim+1].  Stage 2 sums the
+// chunks of each expert in chunk order.  Both orders are fixed.
+constexpr int kChunkRows = 256;
+
+__global__ __launch_bounds__(256) void router_wgrad_partial_kernel(
+    const float* __restrict__ dl, const int32_t* __restrict__ perm,
+    const int32_t* __restrict__ offsets, const uint16_t* __restrict__ x_perm, int dim,
+    int max_chunks, float* __restrict__ partial) {
+  const int e = blockIdx.y;
+  const int c = blockIdx.x;
+  const int r0 = offsets[e] + c * kChunkRows;
+  const int r1 = min(offsets[e + 1], r0 + kChunkRows);
+  float* out = partial + (static_cast<int64_t>(e) * max_chunks + c) * (dim + 1);
+  if (r0 >= offsets[e + 1]) return;  // chunk beyond this expert's rows
+  const int nchunk8 = dim / 8;
+  for (int col8 = threadIdx.x; col8 <= nchunk8; col8 += blockDim.x) {
+    if (col8 == nchunk8) {  // bias column
+      float acc = 0.0f;
+      for (int r = r0; r < r1; ++r) acc = acc + dl[perm[r]];
+      out[dim] = acc;
+    } else {
+      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (int r = r0; r < r1; ++r) {
+        const float g = dl[perm[r]];
+        float xf[8];
+        unpack8(reinterpret_cast<const uint4*>(x_perm + static_cast<int64_t>(r) * dim)[col8], xf);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = fmaf(g, xf[i], acc[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) out[col8 * 8 + i] = acc[i];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void router_wgrad_final_kernel(
+    const float* __restrict__ partial, const int32_t* __restrict__ offsets, int E, int dim,
+    int max_chunks, int grad_dtype, void* __restrict__ dwg, void* __restrict__ dbg) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;  // over E*(dim+1)
+  if (i >= E * (dim + 1)) return;
+  const int e = i / (dim + 1);
+  const int col = i % (dim + 1);
+  const int rows = offsets[e + 1] - offsets[e];
+  const int nch = (rows + kChunkRows - 1) / kChunkRows;
+  float acc = 0.0f;
+  for (int c = 0; c < nch; ++c)
+    acc = acc + partial[(static_cast<int64_t>(e) * max_chunks + c) * (dim + 1) + col];
+  if (col < dim) {
+    const int64_t o = static_cast<int64_t>(e) * dim + col;
+    if (grad_dtype == FMOE_BF16) static_cast<uint16_t*>(dwg)[o] = f2bf(acc);
+    else static_cast<float*>(dwg)[o] = acc;
+  } else {
+    if (grad_dtype == FMOE_BF16) static_cast<uint16_t*>(dbg)[e] = f2bf(acc);
+    else static_cast<float*>(dbg)[e] = acc;
+  }
+}
+
+__global__ void zero_grad_kernel(void* dwg, void* dbg, int E, int dim, int grad_dtype) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= E * (dim + 1)) return;
+  const bool is_w = i < E * dim;
+  void* p = is_w ? dwg : dbg;
+  const int o = is_w ? i : i - E * dim;
+  if (grad_dtype == FMOE_BF16) static_cast<uint16_t*>(p)[o] = 0;
+  else static_cast<float*>(p)[o] = 0.0f;
+}
+
+}  // namespace fmoe
+
+using namespace fmoe;
+
+extern "C" int fmoe_router_fwd(const void* x, const void* gate_w, const void* gate_b, int64_t T,
+                               int64_t dim, int n_experts, int k, float route_scale, int32_t* idx,
+                               int64_t* idx64, float* weights, float* topv, void* stream) {
+  if (T < 0 || dim <= 0) return FMOE_ERR_INVALID_ARG;
+  if (n_experts <= 0 || n_experts > FMOE_MAX_EXPERTS) return FMOE_ERR_TOO_MANY_EXPERTS;
+  if (k <= 0 || k > FMOE_MAX_TOPK || k > n_experts || dim % 64 != 0) return FMOE_ERR_SHAPE;
+  if (T == 0) return FMOE_OK;
+  if (!x || !gate_w || !gate_b || !idx || !weights || !topv) return FMOE_ERR_INVALID_ARG;
+  if (!aligned16(x) || !aligned16(gate_w)) return FMOE_ERR_ALIGN;
+  const int threads = 256;
+  const int64_t blocks = ceil_div(T * kRouterLanes, threads);
+  hipStream_t s = as_stream(stream);
+  auto xs = static_cast<const uint16_t*>(x);
+  auto ws = static_cast<const uint16_t*>(gate_w);
+  auto bs = static_cast<const uint16_t*>(gate_b);
+#define FMOE_ROUTER_LAUNCH(EB)                                                                  \
+  router_fwd_kernel<EB><<<dim3(blocks), dim3(threads), 0, s>>>(xs, ws, bs, (int)T, (int)dim,    \
+                                                               n_experts, k, route_scale, idx,  \
+                                                               idx64, weights, topv)
+  if (n_experts <= 8) FMOE_ROUTER_LAUNCH(8);
+  else if (n_experts <= 16) FMOE_ROUTER_LAUNCH(16);
+  else if (n_experts <= 32) FMOE_ROUTER_LAUNCH(32);
+  else FMOE_ROUTER_LAUNCH(64);
+#undef FMOE_ROUTER_LAUNCH
+  return launch_status();
+}
+
+extern "C" size_t fmoe_router_bwd_workspace_bytes(int64_t T, int64_t dim, int n_experts, int k) {
+  (void)k;
+  if (T <= 0 || dim <= 0 || n_experts <= 0) return 0;
+  const int64_t max_chunks = ceil_div(T, kChunkRows);  // an expert holds at most T rows
+  return static_cast<size_t>(n_experts) * max_chunks * (dim + 1) * sizeof(float);
+}
+
+extern "C" int fmoe_router_bwd(const float* d_weights, const float* topv, const int32_t* perm,
+                               const int32_t* offsets, const void* x_perm, int64_t T, int64_t dim,
+                               int n_experts, int k, float route_scale, float* d_logits,
+                               void* d_gate_w, void* d_gate_b, int grad_dtype, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  if (T < 0 || dim <= 0) return FMOE_ERR_INVALID_ARG;
+  if (n_experts <= 0 || n_experts > FMOE_MAX_EXPERTS) return FMOE_ERR_TOO_MANY_EXPERTS;
+  if (k <= 0 || k > FMOE_MAX_TOPK || k > n_experts || dim % 64 != 0) return FMOE_ERR_SHAPE;
+  if (grad_dtype != FMOE_BF16 && grad_dtype != FMOE_F32) return FMOE_ERR_DTYPE;
+  hipStream_t s = as_stream(stream);
+  if (T == 0) {
+    // No tokens: the gate gradients are zero.
+    if (!d_gate_w || !d_gate_b) return FMOE_ERR_INVALID_ARG;
+    const int64_t n = static_cast<int64_t>(n_experts) * (dim + 1);
+    zero_grad_kernel<<<dim3(ceil_div(n, 256)), dim3(256), 0, s>>>(d_gate_w, d_gate_b,
+                                                                  n_experts, (int)dim, grad_dtype);
+    return launch_status();
+  }
+  if (!d_weights || !topv || !perm || !offsets || !x_perm || !d_logits || !d_gate_w || !d_gate_b ||
+      !workspace)
+    return FMOE_ERR_INVALID_ARG;
+  if (workspace_bytes < fmoe_router_bwd_workspace_bytes(T, dim, n_experts, k))
+    return FMOE_ERR_WORKSPACE;
+  if (!aligned16(x_perm)) return FMOE_ERR_ALIGN;
+  router_dlogit_kernel<<<dim3(ceil_div(T, 256)), dim3(256), 0, s>>>(d_weights, topv, (int)T, k,
+                                                                    route_scale, d_logits);
+  const int max_chunks = static_cast<int>(ceil_div(T, kChunkRows));
+  float* partial = static_cast<float*>(workspace);
+  router_wgrad_partial_kernel<<<dim3(max_chunks, n_experts), dim3(128), 0, s>>>(
+      d_logits, perm, offsets, static_cast<const uint16_t*>(x_perm), (int)dim, max_chunks, partial);
+  const int64_t n = static_cast<int64_t>(n_experts) * (dim + 1);
+  router_wgrad_final_kernel<<<dim3(ceil_div(n, 256)), dim3(256), 0, s>>>(
+      partial, offsets, n_experts, (int)dim, max_chunks, grad_dtype, d_gate_w, d_gate_b);
+  return launch_status();
+}

@@ -1,0 +1,236 @@
+"""Drop-in DeepSeekMoE for MI355X: the reference module's interface over the
+gfx950 kernels of libfusionmoe.so.
+
+Mirrors FusionLLM ``models/moe.py``:
+  * ``SwiGLUExpert`` (moe.py:11-21) — same parameters (w1, w2, w3, bias-free
+    nn.Linear) and the same forward; it is a parameter container for
+    ``DeepSeekMoE`` and is also imported on its own by the reference's MTP
+    module (models/mtp.py:11,28), where it runs as plain torch.
+  * ``DeepSeekMoE`` (moe.py:24-109) — same constructor and config keys
+    (moe.py:27-42), parameter names and init, ``forward`` (moe.py:79-87),
+    ``update_gate_bias`` (moe.py:89-98), ``get_load_balance_loss``
+    (moe.py:100-109), and the ``_last_indices`` / ``_last_weights``
+    attributes (moe.py:41-42,83-84).
+
+``DeepSeekMoE.forward`` runs only on a ROCm device, through the kernels; it
+raises on CPU tensors (there is no CPU fallback).  Numerics follow the
+reference composition with one deliberate change: the router accumulates the
+gate logits in fp32 from the bf16 operands (instead of rounding logits and
+scores to bf16), breaks exact score ties toward the lowest expert index, and
+returns fp32 routing weights.
+
+Supported dtypes: a bf16 module with bf16 input, or any module under
+``torch.autocast("cuda", dtype=torch.bfloat16)`` (the reference trainer's
+mode, training/trainer.py:158), where inputs and weights are used as bf16 and
+gradients come back in each parameter's own dtype.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _kernels as K
+
+
+class SwiGLUExpert(nn.Module):
+    """SwiGLU expert w2(silu(w1 x) * w3 x) (reference: models/moe.py:11-21)."""
+
+    def __init__(self, dim: int, inter_dim: int):
+        super().__init__()
+        self.w1 = nn.Linear(dim, inter_dim, bias=False)
+        self.w2 = nn.Linear(inter_dim, dim, bias=False)
+        self.w3 = nn.Linear(dim, inter_dim, bias=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.w2(F.silu(self.w1(x)) * self.w3(x))
+
+
+def _as_bf16(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)
+
+
+class _MoEBlockFunction(torch.autograd.Function):
+    """Forward and backward of DeepSeekMoE.forward (models/moe.py:79-87) on the kernels.
+
+    Inputs: (meta, x[T,d], gate.weight, gate.bias, *weights) where weights
+    are, per routed expert, (w1, w3, w2) and then the shared expert's
+    (w1, w3, w2) when it exists.  Outputs: y[T,d], indices[T,k] int64,
+    weights[T,k] fp32 (the last two are not differentiable).
+    """
+
+    @staticmethod
+    def forward(ctx, meta, x, gate_w, gate_b, *weights):
+        E, k, inter, rs, has_shared, out_dtype = meta
+        T, d = x.shape
+        xb = _as_bf16(x).contiguous()
+        gwb, gbb = _as_bf16(gate_w).contiguous(), _as_bf16(gate_b).contiguous()
+        wb = [_as_bf16(w).contiguous() for w in weights]
+        G = E + (1 if has_shared else 0)
+        w1s, w3s, w2s = wb[0::3][:G], wb[1::3][:G], wb[2::3][:G]
+
+        idx, idx64, w, v = K.router_fwd(xb, gwb, gbb, k, rs)
+        counts, offsets, perm, pos, x_perm = K.dispatch(idx, xb, E)
+        rows_r, rows_s = T * k, (T if has_shared else 0)
+        ab, h = K.gateup_fwd(x_perm, xb if has_shared else None, offsets, E, w1s, w3s, inter)
+        o = K.down_fwd(h, offsets, E, rows_r, rows_s, w2s, d)
+        y = K.combine_fwd(o, idx, w, pos, rows_r, has_shared, out_dtype)
+
+        # Experts that get no tokens return None gradients (the reference never
+        # puts them in the graph, moe.py:66-72).  Their counts travel to the
+        # host asynchronously and are read at the end of backward.
+        counts_host = torch.empty(E, dtype=torch.int32, pin_memory=True)
+        counts_host.copy_(counts, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+
+        ctx.meta = meta
+        ctx.counts_host = counts_host
+        ctx.counts_event = ev
+        ctx.param_dtypes = (gate_w.dtype, gate_b.dtype, [w.dtype for w in weights])
+        ctx.x_dtype = x.dtype
+        ctx.save_for_backward(xb, gwb, idx, w, v, offsets, perm, pos, x_perm, ab, h, o, *wb)
+        ctx.mark_non_differentiable(idx64, w)
+        return y, idx64, w
+
+    @staticmethod
+    def backward(ctx, dy, _d_idx, _d_w):
+        E, k, inter, rs, has_shared, out_dtype = ctx.meta
+        xb, gwb, idx, w, v, offsets, perm, pos, x_perm, ab, h, o, *wb = ctx.saved_tensors
+        T, d = xb.shape
+        G = E + (1 if has_shared else 0)
+        w1s, w3s, w2s = wb[0::3][:G], wb[1::3][:G], wb[2::3][:G]
+        rows_r, rows_s = T * k, (T if has_shared else 0)
+        gw_dtype, gb_dtype, w_dtypes = ctx.param_dtypes
+
+        dy = dy.contiguous()
+        # Combine backward: routed rows get dy*w (bf16), slots get <dy, o>.
+        d_o, d_w = K.combine_bwd(dy, o, w, perm, k)
+        dy_sh = _as_bf16(dy).contiguous() if has_shared else None
+
+        # Down projection: dX with the SwiGLU backward fused, then dW2.
+        d_ab = K.down_bwd_dx(d_o, dy_sh, offsets, E, w2s, ab, inter)
+        grads_w = [None] * len(wb)
+        dw2 = [torch.empty(d, inter, dtype=w_dtypes[3 * g + 2], device=xb.device) for g in range(G)]
+        K.weight_grad(d_o, dy_sh, h, None, offsets, E, rows_r, rows_s, d, dw2, None,
+                      w_dtypes[2], tag="w2")
+        # Gate/up projections: dX (one product over [w1; w3]) then dW1, dW3.
+        dx_rows = K.gateup_bwd_dx(d_ab, offsets, E, rows_r, rows_s, w1s, w3s, d)
+        dw1 = [torch.empty(inter, d, dtype=w_dtypes[3 * g], device=xb.device) for g in range(G)]
+        dw3 = [torch.empty(inter, d, dtype=w_dtypes[3 * g + 1], device=xb.device) for g in range(G)]
+        K.weight_grad(d_ab, None, x_perm, xb if has_shared else None, offsets, E, rows_r, rows_s,
+                      inter, dw1, dw3, w_dtypes[0], tag="w13")
+        # Router: logits gradient, gate weight/bias gradient.
+        d_logits, dgw, dgb = K.router_bwd(d_w, v, perm, offsets, x_perm, E, rs, gw_dtype)
+        if dgb.dtype != gb_dtype:
+            dgb = dgb.to(gb_dtype)
+        dx = None
+        if ctx.needs_input_grad[1]:
+            dx = K.dx_reduce(dx_rows, pos, idx, d_logits, gwb, rows_r, has_shared, ctx.x_dtype)
+
+        ctx.counts_event.synchronize()
+        counts = ctx.counts_host.tolist()
+        for g in range(G):
+            if g < E and counts[g] == 0:
+                continue
+            grads_w[3 * g], grads_w[3 * g + 1], grads_w[3 * g + 2] = dw1[g], dw3[g], dw2[g]
+        return (None, dx, dgw, dgb, *grads_w)
+
+
+class DeepSeekMoE(nn.Module):
+    """DeepSeekMoE with aux-loss-free biased sigmoid routing (reference: models/moe.py:24-109)."""
+
+    def __init__(self, config: dict):
+        super().__init__()
+        self.dim = config["dim"]
+        self.n_routed_experts = config["n_routed_experts"]
+        self.n_shared_experts = config["n_shared_experts"]
+        self.n_activated_experts = config["n_activated_experts"]
+        self.moe_inter_dim = config["moe_inter_dim"]
+        self.route_scale = config.get("route_scale", 1.0)
+
+        self.gate = nn.Linear(self.dim, self.n_routed_experts, bias=True)
+        nn.init.zeros_(self.gate.bias)
+        nn.init.normal_(self.gate.weight, std=0.006)
+        self.experts = nn.ModuleList(
+            [SwiGLUExpert(self.dim, self.moe_inter_dim) for _ in range(self.n_routed_experts)])
+        # As in the reference, n_shared_experts > 0 means one shared expert.
+        self.shared_expert = SwiGLUExpert(self.dim, self.moe_inter_dim) if self.n_shared_experts > 0 else None
+        self._last_indices: torch.Tensor | None = None
+        self._last_weights: torch.Tensor | None = None
+
+    def _flat_weights(self) -> list[torch.Tensor]:
+        ws = []
+        mods = list(self.experts) + ([self.shared_expert] if self.shared_expert is not None else [])
+        for m in mods:
+            ws += [m.w1.weight, m.w3.weight, m.w2.weight]
+        return ws
+
+    def _output_dtype(self, x: torch.Tensor) -> torch.dtype:
+        params_bf16 = all(p.dtype == torch.bfloat16 for p in self.parameters())
+        if torch.is_autocast_enabled("cuda"):
+            if torch.get_autocast_dtype("cuda") != torch.bfloat16:
+                raise NotImplementedError("fusionllm_amd.DeepSeekMoE supports bf16 autocast only")
+            if x.dtype not in (torch.bfloat16, torch.float32):
+                raise NotImplementedError(f"unsupported input dtype {x.dtype}")
+            return x.dtype  # promote(x.dtype, bf16 shared output) for fp32 / bf16 x
+        if x.dtype == torch.bfloat16 and params_bf16:
+            return torch.bfloat16
+        raise NotImplementedError(
+            "fusionllm_amd.DeepSeekMoE computes in bf16: use a bf16 module with bf16 input, or run "
+            "under torch.autocast('cuda', dtype=torch.bfloat16)")
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        shape = x.shape
+        flat = x.view(-1, self.dim)
+        if not flat.is_cuda:
+            raise RuntimeError("fusionllm_amd.DeepSeekMoE runs on a ROCm device only (got a CPU tensor)")
+        out_dtype = self._output_dtype(flat)
+        E, k = self.n_routed_experts, self.n_activated_experts
+        if flat.shape[0] == 0:
+            return self._forward_empty(flat, out_dtype).view(shape)
+        meta = (E, k, self.moe_inter_dim, float(self.route_scale), self.shared_expert is not None, out_dtype)
+        with torch.cuda.device(flat.device):
+            y, idx64, w = _MoEBlockFunction.apply(meta, flat, self.gate.weight, self.gate.bias,
+                                                  *self._flat_weights())
+        self._last_indices = idx64
+        self._last_weights = w
+        return y.view(shape)
+
+    def _forward_empty(self, flat: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
+        # Zero tokens: nothing to compute.  Keep the output connected to the
+        # gate and shared-expert parameters so autograd yields zero (not None)
+        # gradients for them, as the reference's empty matmuls do.
+        k = self.n_activated_experts
+        self._last_indices = torch.empty(0, k, dtype=torch.int64, device=flat.device)
+        self._last_weights = torch.empty(0, k, dtype=torch.float32, device=flat.device)
+        y = flat.new_zeros(0, self.dim, dtype=out_dtype)
+        tied = [self.gate.weight, self.gate.bias]
+        if self.shared_expert is not None:
+            tied += [self.shared_expert.w1.weight, self.shared_expert.w2.weight, self.shared_expert.w3.weight]
+        return y + sum(p.sum() * 0 for p in tied).to(out_dtype) + flat.sum().to(out_dtype) * 0
+
+    def update_gate_bias(self, speed: float = 0.001) -> None:
+        """Load-balancing bias step from the last routing (reference: models/moe.py:89-98)."""
+        if self._last_indices is None:
+            return
+        load = torch.bincount(self._last_indices.flatten(), minlength=self.n_routed_experts).float()
+        mean = load.mean()
+        overloaded = load > mean * 1.10
+        underloaded = load < mean * 0.90
+        with torch.no_grad():
+            self.gate.bias[overloaded] -= speed
+            self.gate.bias[underloaded] += speed
+
+    def get_load_balance_loss(self) -> torch.Tensor:
+        """Diagnostic load-balance loss from the last routing (reference: models/moe.py:100-109)."""
+        if self._last_indices is None or self._last_weights is None:
+            return torch.tensor(0.0, device=self.gate.weight.device)
+        T, k = self._last_weights.shape
+        E = self.n_routed_experts
+        flat_idx = self._last_indices.flatten()
+        load = torch.bincount(flat_idx, minlength=E).float()
+        frac = load / (load.sum() + 1e-10)
+        onehot = F.one_hot(flat_idx, num_classes=E).float()
+        prob = (onehot * self._last_weights.flatten().unsqueeze(-1)).view(T, k, E).sum(dim=1).mean(dim=0)
+        return (frac * prob).sum() * E

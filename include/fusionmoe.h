@@ -1,0 +1,231 @@
+/*
+ * fusionmoe.h — C ABI of libfusionmoe.so, the gfx950 (MI355X) kernels behind
+ * the DeepSeekMoE feed-forward block of FusionLLM.
+ *
+ * The reference (FusionLLM models/moe.py) has no FFI: its boundary is the
+ * nn.Module API of DeepSeekMoE.  Each entry point below replaces one stretch
+ * of that module's torch-op sequence; the citation on each names the lines.
+ * The host side (fusionllm_amd/moe.py) binds these with ctypes and keeps the
+ * reference's module interface (constructor, parameter names, forward,
+ * update_gate_bias, get_load_balance_loss, _last_indices/_last_weights).
+ *
+ * Conventions shared by every entry point
+ *   - Plain pointers and sizes only; every device pointer is borrowed.  The
+ *     library never allocates or frees device memory: outputs and workspaces
+ *     are caller-allocated (sizes from the *_workspace_bytes queries).
+ *   - Every call is asynchronous on `stream` (a hipStream_t passed as void*;
+ *     NULL is the legacy default stream).  No call synchronises the device.
+ *   - Return value: FMOE_OK (0) or a nonzero status; fmoe_status_string()
+ *     names it.  Nothing throws or aborts across the ABI.
+ *   - Matrices are row-major and densely packed unless a leading dimension
+ *     is passed.  bf16 is stored as 16-bit IEEE bfloat16 bit patterns.
+ *   - "Rows" of the expert buffers: the routed slots in expert-major,
+ *     token-ascending order (rows 0 .. rows_routed-1, rows_routed = T*k),
+ *     followed by rows_shared rows for the shared expert (rows_shared = T,
+ *     or 0 when the block has no shared expert).  Expert e owns rows
+ *     offsets[e] .. offsets[e+1]-1; offsets[] lives in device memory and is
+ *     produced by fmoe_dispatch, so no host synchronisation is needed.
+ *   - Per-expert weights are passed as HOST arrays of device pointers, one
+ *     entry per routed expert followed by one for the shared expert (when
+ *     rows_shared > 0).  Each weight is the nn.Linear weight of the
+ *     reference: w1, w3 are [inter, dim], w2 is [dim, inter].
+ *   - dim and inter must be multiples of 64; n_experts <= FMOE_MAX_EXPERTS.
+ */
+#ifndef FUSIONMOE_H
+#define FUSIONMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FMOE_ABI_VERSION 1
+#define FMOE_MAX_EXPERTS 64
+#define FMOE_MAX_TOPK 8
+
+enum fmoe_status {
+  FMOE_OK = 0,
+  FMOE_ERR_INVALID_ARG = 1,   /* null pointer or negative size */
+  FMOE_ERR_SHAPE = 2,         /* unsupported dimension (not a multiple of 64, k > E, ...) */
+  FMOE_ERR_ALIGN = 3,         /* pointer not 16-byte aligned */
+  FMOE_ERR_DTYPE = 4,         /* unknown dtype code */
+  FMOE_ERR_LAUNCH = 5,        /* hipGetLastError after a launch */
+  FMOE_ERR_WORKSPACE = 6,     /* workspace smaller than the size query returned */
+  FMOE_ERR_TOO_MANY_EXPERTS = 7
+};
+
+enum fmoe_dtype { FMOE_BF16 = 0, FMOE_F32 = 1 };
+
+/* ABI version of the loaded library (FMOE_ABI_VERSION at build time). */
+int fmoe_abi_version(void);
+
+/* Static, human-readable text for a status code. */
+const char* fmoe_status_string(int status);
+
+/* ---------------------------------------------------------------------------
+ * Routing.  Replaces DeepSeekMoE._route (models/moe.py:44-50):
+ *   logits = gate(x) (moe.py:46), scores = sigmoid(logits) (:47),
+ *   (v, idx) = topk(scores, k) (:48), w = v / (sum(v) + 1e-10) * route_scale (:49).
+ * x [T, dim], gate_w [E, dim], gate_b [E] are bf16.  Logits are accumulated
+ * in fp32 (products of bf16 operands are exact in fp32) in a fixed order, the
+ * score is 1/(1+exp(-logit)), and top-k picks the k largest scores in
+ * descending order, ties to the lowest expert index, NaN above every number.
+ * Outputs: idx [T,k] int32, idx64 [T,k] int64 (may be NULL; it backs
+ * DeepSeekMoE._last_indices, moe.py:83), weights [T,k] fp32 (moe.py:84),
+ * topv [T,k] fp32 (the selected scores, kept for the backward pass).
+ * ------------------------------------------------------------------------- */
+int fmoe_router_fwd(const void* x, const void* gate_w, const void* gate_b,
+                    int64_t T, int64_t dim, int n_experts, int k, float route_scale,
+                    int32_t* idx, int64_t* idx64, float* weights, float* topv,
+                    void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Dispatch.  Replaces the permutation half of
+ * DeepSeekMoE._dispatch_scatter_gather (models/moe.py:55-64) and the per-expert
+ * row gathers x[token_ids] (moe.py:73,75):
+ *   expert-count histogram -> exclusive scan -> stable counting-sort scatter
+ *   -> gather of x rows into an expert-contiguous buffer.
+ * Slot s = t*k + j is token t's j-th choice.  Outputs:
+ *   counts [E] int32, offsets [E+1] int32 (exclusive scan of counts),
+ *   perm [T*k] int32 (row -> slot, expert-major, slot-ascending; equals
+ *   torch.argsort(idx.flatten(), stable=True)),
+ *   pos_of_slot [T*k] int32 (slot -> row, the inverse of perm),
+ *   x_perm [T*k, dim] bf16 (row r holds x[perm[r] / k]).
+ * ------------------------------------------------------------------------- */
+size_t fmoe_dispatch_workspace_bytes(int64_t T, int n_experts, int k);
+int fmoe_dispatch(const int32_t* idx, const void* x, int64_t T, int64_t dim,
+                  int n_experts, int k,
+                  int32_t* counts, int32_t* offsets, int32_t* perm,
+                  int32_t* pos_of_slot, void* x_perm,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Grouped gate/up projection with the SwiGLU product fused in the epilogue.
+ * Replaces w1(x), w3(x), F.silu and * of SwiGLUExpert.forward
+ * (models/moe.py:21) for every active expert of the loop at moe.py:66-76 and
+ * for the shared expert (moe.py:86), as one launch.
+ *   a = x_e w1_e^T, b = x_e w3_e^T (bf16-rounded, as nn.Linear returns),
+ *   h = bf16(bf16(silu(a)) * b).
+ * x_routed: [rows_routed, dim] (x_perm from fmoe_dispatch); x_shared: [T, dim].
+ * Outputs over all rows: ab [rows, 2*inter] (a in columns 0..inter-1, b in
+ * inter..2*inter-1; kept for the backward pass), h [rows, inter].
+ * ------------------------------------------------------------------------- */
+int fmoe_gateup_fwd(const void* x_routed, const void* x_shared,
+                    const int32_t* offsets, int n_experts,
+                    int64_t rows_routed, int64_t rows_shared,
+                    int64_t dim, int64_t inter,
+                    const void* const* w1, const void* const* w3,
+                    void* ab, void* h, void* stream);
+
+/* Grouped down projection w2(h) of SwiGLUExpert.forward (models/moe.py:21),
+ * all experts plus the shared expert in one launch.  h: [rows, inter];
+ * out: [rows, dim] bf16. */
+int fmoe_down_fwd(const void* h, const int32_t* offsets, int n_experts,
+                  int64_t rows_routed, int64_t rows_shared,
+                  int64_t dim, int64_t inter, const void* const* w2,
+                  void* out, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Weighted combine fused with the shared-expert add.  Replaces
+ * y.index_add_(0, token_ids, (expert_out * w).to(fp32)) over the experts in
+ * ascending order (models/moe.py:65-76), y.to(x.dtype) (:77) and
+ * y_routed + y_shared (:87).  Per token, in fp32 and ascending expert order:
+ *   acc = 0; acc = acc + (o_j * w_j)  (product rounded, then the add)
+ * then y = out_dtype(acc) + shared (bf16 add for FMOE_BF16; for FMOE_F32 the
+ * fp32 sum acc + shared, the autocast case where x is fp32).
+ * Deterministic: token-major gather, no atomics.
+ * expert_out: [rows_routed + rows_shared, dim] bf16 (from fmoe_down_fwd).
+ * ------------------------------------------------------------------------- */
+int fmoe_combine_fwd(const void* expert_out, const int32_t* idx,
+                     const float* weights, const int32_t* pos_of_slot,
+                     int64_t T, int64_t dim, int k, int64_t rows_routed,
+                     int has_shared, int out_dtype, void* y, void* stream);
+
+/* Backward of the combine (autograd of moe.py:76-77,87):
+ *   d_expert_out[r] = bf16(dy[t] * w_slot)   for routed row r (slot perm[r]),
+ *   d_weights[slot]  = sum_c dy[t,c] * o[r,c]  (fp32).
+ * dy: [T, dim] of dy_dtype; d_expert_out: [rows_routed, dim] bf16;
+ * d_weights: [T, k] fp32. */
+int fmoe_combine_bwd(const void* dy, int dy_dtype, const void* expert_out,
+                     const float* weights, const int32_t* perm,
+                     int64_t T, int64_t dim, int k,
+                     void* d_expert_out, float* d_weights, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Backward of SwiGLUExpert (autograd of models/moe.py:21), grouped like the
+ * forward.  fmoe_down_bwd_dx: dh = d_out w2 (bf16-rounded), then the SwiGLU
+ * backward in the epilogue:  da = bf16(bf16(dh*b) * silu'(a)),
+ * db = bf16(dh * bf16(silu(a))).  d_out_routed: [rows_routed, dim];
+ * d_out_shared: [rows_shared, dim]; ab from fmoe_gateup_fwd; d_ab: [rows, 2*inter].
+ * ------------------------------------------------------------------------- */
+int fmoe_down_bwd_dx(const void* d_out_routed, const void* d_out_shared,
+                     const int32_t* offsets, int n_experts,
+                     int64_t rows_routed, int64_t rows_shared,
+                     int64_t dim, int64_t inter, const void* const* w2,
+                     const void* ab, void* d_ab, void* stream);
+
+/* dx_rows = da w1 + db w3 for every row (one product over K = 2*inter);
+ * dx_rows: [rows, dim] bf16. */
+int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int n_experts,
+                       int64_t rows_routed, int64_t rows_shared,
+                       int64_t dim, int64_t inter,
+                       const void* const* w1, const void* const* w3,
+                       void* dx_rows, void* stream);
+
+/* Grouped weight gradient, the dW half of nn.Linear backward for every expert:
+ *   G_e = A_e^T B_e,  A_e = rows of expert e of A ([*, m_out]),
+ *                     B_e = the same rows of B ([*, n_out]).
+ * Row i < m_split of G_e goes to out_lo[e] ([m_split, n_out]); rows >= m_split
+ * go to out_hi[e] ([m_out - m_split, n_out]).  out dtype bf16 or f32.
+ * For w2: A = d_out, B = h, m_split = m_out = dim.  For w1/w3: A = d_ab,
+ * B = x, m_split = inter (out_lo = dw1, out_hi = dw3).
+ * The reduction over rows is split into fixed chunks summed in chunk order,
+ * so the result is deterministic.  Experts with no rows are left untouched
+ * (the reference leaves their .grad as None, moe.py:66-72). */
+size_t fmoe_weight_grad_workspace_bytes(int64_t rows_routed, int64_t rows_shared,
+                                        int n_experts, int64_t m_out, int64_t n_out);
+int fmoe_weight_grad(const void* a_routed, const void* a_shared, int64_t lda,
+                     const void* b_routed, const void* b_shared, int64_t ldb,
+                     const int32_t* offsets, int n_experts,
+                     int64_t rows_routed, int64_t rows_shared,
+                     int64_t m_out, int64_t n_out, int64_t m_split,
+                     void* const* out_lo, void* const* out_hi, int out_dtype,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Router backward (autograd of models/moe.py:46-49): normalisation backward,
+ * top-k scatter, sigmoid backward, then the gate Linear's weight and bias
+ * gradients.  d_logits [T,k] fp32 holds dL/dlogit for each selected expert
+ * (the other logits get zero gradient); d_gate_w [E, dim] and d_gate_b [E]
+ * are written in grad_dtype.  The reductions over tokens run over x_perm in
+ * expert-contiguous order with a fixed chunking: deterministic.
+ * ------------------------------------------------------------------------- */
+size_t fmoe_router_bwd_workspace_bytes(int64_t T, int64_t dim, int n_experts, int k);
+int fmoe_router_bwd(const float* d_weights, const float* topv,
+                    const int32_t* perm, const int32_t* offsets,
+                    const void* x_perm, int64_t T, int64_t dim,
+                    int n_experts, int k, float route_scale,
+                    float* d_logits, void* d_gate_w, void* d_gate_b,
+                    int grad_dtype, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/* Input gradient of the block: the backward of every use of x in
+ * DeepSeekMoE.forward (x[token_ids] at moe.py:75, the gate at :46, the shared
+ * expert at :86), summed per token in fp32 in a fixed order:
+ *   dx[t] = sum_j dx_rows[pos_of_slot[t*k+j]]  (ascending expert)
+ *         + dx_rows[rows_routed + t] (shared, if has_shared)
+ *         + sum_j d_logits[t,j] * gate_w[idx[t,j]]
+ * written in out_dtype. */
+int fmoe_dx_reduce(const void* dx_rows, const int32_t* pos_of_slot,
+                   const int32_t* idx, const float* d_logits,
+                   const void* gate_w, int64_t T, int64_t dim, int k,
+                   int64_t rows_routed, int has_shared, int out_dtype,
+                   void* dx, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FUSIONMOE_H */

