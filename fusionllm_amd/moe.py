@@ -91,11 +91,16 @@ class _MoEBlockFunction(torch.autograd.Function):
         ctx.x_dtype = x.dtype
         ctx.save_for_backward(xb, gwb, idx, w, v, offsets, perm, pos, x_perm, ab, h, o, *wb)
         ctx.mark_non_differentiable(idx64, w)
+        # The index and weight outputs never carry gradients: do not let
+        # autograd fill zero tensors for them.
+        ctx.set_materialize_grads(False)
         return y, idx64, w
 
     @staticmethod
     def backward(ctx, dy, _d_idx, _d_w):
         E, k, inter, rs, has_shared, out_dtype = ctx.meta
+        if dy is None:  # y did not reach the loss
+            return (None,) * (4 + len(ctx.param_dtypes[2]))
         xb, gwb, idx, w, v, offsets, perm, pos, x_perm, ab, h, o, *wb = ctx.saved_tensors
         T, d = xb.shape
         G = E + (1 if has_shared else 0)

@@ -48,10 +48,11 @@ def route(x, gate_w, gate_b, k: int, route_scale: float = 1.0, mode: str = "fp32
     and keeps the weights differentiable: topk's backward scatters into the
     selected scores, which is what gathering them does.
     """
+    wide = torch.float64 if x.dtype == torch.float64 else torch.float32  # fp64 ground truth stays fp64
     if indices is not None:
         if mode != "fp32":
             raise ValueError("indices= needs mode='fp32'")
-        scores = torch.sigmoid(F.linear(x.float(), gate_w.float(), gate_b.float()))
+        scores = torch.sigmoid(F.linear(x.to(wide), gate_w.to(wide), gate_b.to(wide)))
         weights = scores.gather(-1, indices.long())
         weights = weights / (weights.sum(dim=-1, keepdim=True) + 1e-10) * route_scale
         return weights, indices.long()
@@ -60,7 +61,7 @@ def route(x, gate_w, gate_b, k: int, route_scale: float = 1.0, mode: str = "fp32
         scores = torch.sigmoid(logits)                            # moe.py:47
         weights, indices = torch.topk(scores, k=k, dim=-1)        # moe.py:48
     elif mode == "fp32":
-        logits = F.linear(x.float(), gate_w.float(), gate_b.float())
+        logits = F.linear(x.to(wide), gate_w.to(wide), gate_b.to(wide))
         scores = torch.sigmoid(logits)
         weights, indices = topk_lowest_index(scores, k)
     else:
