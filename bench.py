@@ -66,6 +66,7 @@ def kernel_model(cfg, T):
         "combine_bwd": ("hbm", T * k * (2 * d + 2 * d + 2 * d + 4 + 4 + 4)),
         "router_bwd": ("hbm", T * k * (2 * d + 4 * 4)),
         "dx_reduce": ("hbm", T * (k * 2 * d + 2 * d + 2 * d + 12 * k)),
+        "transpose_weights": ("hbm", (E + (1 if cfg.n_shared else 0)) * 3 * d * I * 2 * 2),
     }
 
 

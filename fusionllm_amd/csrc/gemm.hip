@@ -145,6 +145,11 @@ __device__ __forceinline__ void mma_ktile(const uint8_t* sA, const uint8_t* sB,
 }
 
 // ---- row-grouped products ---------------------------------------------------
+// Every row-grouped product streams both operands K-contiguous: the
+// activations are row-major [rows, K]; the weights are nn.Linear weights
+// ([out, in], K = in) for the forward products and the transposed copies made
+// by fmoe_transpose_weights for the backward ones (w2t for dh = d_out * w2,
+// w13t for dx = [da | db] * [w1; w3]).
 enum GemmMode { GATEUP_FWD = 0, DOWN_FWD = 1, DOWN_BWD = 2, GATEUP_BWD = 3 };
 
 struct GemmArgs {
@@ -157,18 +162,28 @@ struct GemmArgs {
   int rows_shared;
   int K;        // reduction length
   int N;        // output columns (GATEUP_FWD: inter = h columns)
-  int inter;    // SwiGLU width (GATEUP_FWD, DOWN_BWD, GATEUP_BWD)
-  int64_t ldb;  // leading dimension of the weights
+  int inter;    // SwiGLU width (GATEUP_FWD, DOWN_BWD)
+  int64_t ldb;  // leading dimension of the (K-contiguous) weight operand
   uint16_t* c0;  // main output (ab / out / d_ab / dx_rows)
   uint16_t* c1;  // GATEUP_FWD: h
   const uint16_t* aux;  // DOWN_BWD: ab
   int64_t ldc0, ldc1, ldaux;
-  const uint16_t* b0[FMOE_MAX_EXPERTS + 1];  // w1 / w2 / w2 / w1
-  const uint16_t* b1[FMOE_MAX_EXPERTS + 1];  // w3 / - / - / w3
+  const uint16_t* b0[FMOE_MAX_EXPERTS + 1];  // w1 / w2 / w2t / w13t
+  const uint16_t* b1[FMOE_MAX_EXPERTS + 1];  // w3 (GATEUP_FWD only)
 };
+
+// Epilogue staging: the tile's bf16 values in LDS, row-major with 512 bytes
+// per row; 16-byte chunk c of row r sits at chunk position c ^ (r & 31), so
+// both the MFMA-layout 2-byte writes and the row-chunk 16-byte reads are free
+// of bank conflicts.
+__device__ __forceinline__ uint32_t stage_off(int row, int col) {
+  return static_cast<uint32_t>(row) * 512u +
+         (static_cast<uint32_t>((col >> 3) ^ (row & 31)) << 4) + static_cast<uint32_t>(col & 7) * 2u;
+}
 
 template <class C, int MODE>
 __global__ __launch_bounds__(C::NT) void grouped_gemm_kernel(const GemmArgs args) {
+  static_assert(C::BM == 256 && C::BN == 256, "epilogue staging assumes a 256 x 256 tile");
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::STAGE_BYTES];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
@@ -203,7 +218,7 @@ __global__ __launch_bounds__(C::NT) void grouped_gemm_kernel(const GemmArgs args
                           ? args.a_routed + static_cast<int64_t>(row_base) * args.lda
                           : args.a_shared;
 
-  // ---- operand loaders
+  // ---- operand loaders (both K-contiguous)
   KLoad<C::BM, C::NT> la;
 #pragma unroll
   for (int i = 0; i < la.PER; ++i) {
@@ -211,53 +226,31 @@ __global__ __launch_bounds__(C::NT) void grouped_gemm_kernel(const GemmArgs args
     r = r < M ? r : M - 1;
     la.src[i] = A + static_cast<int64_t>(r) * args.lda + KLoad<C::BM, C::NT>::chunk_of(tid) * 8;
   }
-  constexpr bool B_KMAJOR = (MODE == GATEUP_FWD || MODE == DOWN_FWD);
-  KLoad<C::BN, C::NT> lbk;
-  constexpr int B_NTL = C::NT < C::BN ? C::NT : C::BN;
-  MNLoad<C::BN, B_NTL> lbm;
-  const int b_ltid = tid - (C::NT - B_NTL);
+  KLoad<C::BN, C::NT> lb;
   const uint16_t* W0 = args.b0[g];
   const uint16_t* W1 = args.b1[g];
-  if constexpr (B_KMAJOR) {
 #pragma unroll
-    for (int i = 0; i < lbk.PER; ++i) {
-      const int r = KLoad<C::BN, C::NT>::row_of(tid, i);
-      const uint16_t* base;
-      int n;
-      if constexpr (MODE == GATEUP_FWD) {
-        // accumulator column block fn of wave column wb: even fn -> w1, odd -> w3,
-        // both for h columns n0 + wb*WTN/2 + (fn/2)*32 + i.
-        const int wb = r / C::WTN, within = r % C::WTN, fn = within / 32;
-        n = n0 + wb * (C::WTN / 2) + (fn / 2) * 32 + (within % 32);
-        base = (fn & 1) ? W1 : W0;
-      } else {
-        n = n0 + r;
-        base = W0;
-      }
-      n = n < args.N ? n : args.N - 1;
-      lbk.src[i] = base + static_cast<int64_t>(n) * args.ldb + KLoad<C::BN, C::NT>::chunk_of(tid) * 8;
-    }
-  }
-  auto b_rowptr = [&](int k) -> const uint16_t* {
-    if constexpr (MODE == GATEUP_BWD) {
-      // K runs over [w1 rows | w3 rows] (2*inter), each row of length N = dim.
-      return k < args.inter ? W0 + static_cast<int64_t>(k) * args.ldb
-                            : W1 + static_cast<int64_t>(k - args.inter) * args.ldb;
+  for (int i = 0; i < lb.PER; ++i) {
+    const int r = KLoad<C::BN, C::NT>::row_of(tid, i);
+    const uint16_t* base = W0;
+    int n;
+    if constexpr (MODE == GATEUP_FWD) {
+      // accumulator column block fn of wave column wb: even fn -> w1, odd -> w3,
+      // both for h columns n0 + wb*WTN/2 + (fn/2)*32 + i.
+      const int wb = r / C::WTN, within = r % C::WTN, fn = within / 32;
+      n = n0 + wb * (C::WTN / 2) + (fn / 2) * 32 + (within % 32);
+      base = (fn & 1) ? W1 : W0;
     } else {
-      return W0 + static_cast<int64_t>(k) * args.ldb;
+      n = n0 + r;
     }
-  };
+    n = n < args.N ? n : args.N - 1;
+    lb.src[i] = base + static_cast<int64_t>(n) * args.ldb + KLoad<C::BN, C::NT>::chunk_of(tid) * 8;
+  }
 
-  auto load_tile = [&](int k0) {
-    la.load(k0);
-    if constexpr (B_KMAJOR) lbk.load(k0);
-    else lbm.load(b_ltid, k0, n0, args.N, b_rowptr);
-  };
   auto store_tile = [&](int buf) {
     uint8_t* sA = smem + buf * C::STAGE_BYTES;
     la.store(sA, tid);
-    if constexpr (B_KMAJOR) lbk.store(sA + C::A_BYTES, tid);
-    else lbm.store(sA + C::A_BYTES, b_ltid);
+    lb.store(sA + C::A_BYTES, tid);
   };
 
   f32x16 acc[C::FM][C::FN];
@@ -269,68 +262,92 @@ __global__ __launch_bounds__(C::NT) void grouped_gemm_kernel(const GemmArgs args
       for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
 
   const int nk = args.K / kBK;
-  load_tile(0);
+  la.load(0);
+  lb.load(0);
   store_tile(0);
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = kt & 1;
-    if (kt + 1 < nk) load_tile((kt + 1) * kBK);
+    if (kt + 1 < nk) {
+      la.load((kt + 1) * kBK);
+      lb.load((kt + 1) * kBK);
+    }
     const uint8_t* sA = smem + buf * C::STAGE_BYTES;
     mma_ktile<C>(sA, sA + C::A_BYTES, acc, wm, wn, lane);
     if (kt + 1 < nk) store_tile(buf ^ 1);
     __syncthreads();
   }
 
-  // ---- epilogue
+  // ---- epilogue, phase 1: bf16-rounded accumulators into the LDS stage
+  // (the loop ended with a barrier, so both operand stages are free).
+  // GATEUP_FWD stages a in columns 0..127 and b in 128..255 (h column order).
+  uint8_t* cs = smem;
   const int row_l = (lane >> 5) * 4;
-  if constexpr (MODE == GATEUP_FWD) {
 #pragma unroll
-    for (int fm = 0; fm < C::FM; ++fm) {
+  for (int fm = 0; fm < C::FM; ++fm) {
 #pragma unroll
-      for (int p = 0; p < C::FN / 2; ++p) {
-        const int col = n0 + wn * (C::WTN / 2) + p * 32 + (lane & 31);
-        if (col >= args.N) continue;
+    for (int fn = 0; fn < C::FN; ++fn) {
+      int col;
+      if constexpr (MODE == GATEUP_FWD)
+        col = (fn & 1) * 128 + wn * (C::WTN / 2) + (fn / 2) * 32 + (lane & 31);
+      else
+        col = wn * C::WTN + fn * 32 + (lane & 31);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm * C::WTM + fm * 32 + (r >> 2) * 8 + row_l + (r & 3);
-          if (m >= M) continue;
-          const float a = bf_round(acc[fm][2 * p][r]);
-          const float b = bf_round(acc[fm][2 * p + 1][r]);
-          const float s = bf_round(a * fast_sigmoid(a));
-          const int64_t row = row_base + m;
-          args.c0[row * args.ldc0 + col] = f2bf(a);
-          args.c0[row * args.ldc0 + args.inter + col] = f2bf(b);
-          args.c1[row * args.ldc1 + col] = f2bf(s * b);
-        }
+      for (int r = 0; r < 16; ++r) {
+        const int row = wm * C::WTM + fm * 32 + (r >> 2) * 8 + row_l + (r & 3);
+        *reinterpret_cast<uint16_t*>(cs + stage_off(row, col)) = f2bf(acc[fm][fn][r]);
       }
     }
+  }
+  __syncthreads();
+
+  // ---- epilogue, phase 2: 16-byte chunks of whole rows
+  if constexpr (MODE == GATEUP_FWD) {
+    // 256 rows x 16 chunks of h; a chunk c pairs a (staged chunk c) and b (16 + c)
+    for (int idx = tid; idx < C::BM * 16; idx += C::NT) {
+      const int row = idx >> 4, c = idx & 15;
+      const int col = n0 + c * 8;
+      if (m0 + row >= M || col >= args.N) continue;
+      const uint4 av = *reinterpret_cast<const uint4*>(cs + stage_off(row, c * 8));
+      const uint4 bv = *reinterpret_cast<const uint4*>(cs + stage_off(row, 128 + c * 8));
+      float af[8], bfv[8], hf[8];
+      unpack8(av, af);
+      unpack8(bv, bfv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) hf[i] = bf_round(af[i] * fast_sigmoid(af[i])) * bfv[i];
+      const int64_t grow = row_base + m0 + row;
+      *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + col) = av;
+      *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + args.inter + col) = bv;
+      *reinterpret_cast<uint4*>(args.c1 + grow * args.ldc1 + col) = pack8(hf);
+    }
   } else {
+    for (int idx = tid; idx < C::BM * 32; idx += C::NT) {
+      const int row = idx >> 5, c = idx & 31;
+      const int col = n0 + c * 8;
+      if (m0 + row >= M || col >= args.N) continue;
+      const uint4 v = *reinterpret_cast<const uint4*>(cs + stage_off(row, c * 8));
+      const int64_t grow = row_base + m0 + row;
+      if constexpr (MODE == DOWN_BWD) {
+        // h = s * b with s = bf16(silu(a)); dh arrives bf16-rounded:
+        // da = bf16(bf16(dh * b) * silu'(a)), db = bf16(dh * s)
+        const uint4 avv = *reinterpret_cast<const uint4*>(args.aux + grow * args.ldaux + col);
+        const uint4 bvv = *reinterpret_cast<const uint4*>(args.aux + grow * args.ldaux + args.inter + col);
+        float dh[8], af[8], bfv[8], da[8], db[8];
+        unpack8(v, dh);
+        unpack8(avv, af);
+        unpack8(bvv, bfv);
 #pragma unroll
-    for (int fm = 0; fm < C::FM; ++fm) {
-#pragma unroll
-      for (int fn = 0; fn < C::FN; ++fn) {
-        const int col = n0 + wn * C::WTN + fn * 32 + (lane & 31);
-        if (col >= args.N) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm * C::WTM + fm * 32 + (r >> 2) * 8 + row_l + (r & 3);
-          if (m >= M) continue;
-          const int64_t row = row_base + m;
-          if constexpr (MODE == DOWN_BWD) {
-            // h = s * b with s = bf16(silu(a)); dh arrives bf16-rounded.
-            const float dh = bf_round(acc[fm][fn][r]);
-            const float a = bf2f(args.aux[row * args.ldaux + col]);
-            const float b = bf2f(args.aux[row * args.ldaux + args.inter + col]);
-            const float sg = fast_sigmoid(a);
-            const float s = bf_round(a * sg);
-            const float ds = bf_round(dh * b);
-            const float da = ds * (sg * (1.0f + a * (1.0f - sg)));
-            args.c0[row * args.ldc0 + col] = f2bf(da);
-            args.c0[row * args.ldc0 + args.inter + col] = f2bf(dh * s);
-          } else {
-            args.c0[row * args.ldc0 + col] = f2bf(acc[fm][fn][r]);
-          }
+        for (int i = 0; i < 8; ++i) {
+          const float sg = fast_sigmoid(af[i]);
+          const float sv = bf_round(af[i] * sg);
+          const float ds = bf_round(dh[i] * bfv[i]);
+          da[i] = ds * (sg * (1.0f + af[i] * (1.0f - sg)));
+          db[i] = dh[i] * sv;
         }
+        *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + col) = pack8(da);
+        *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + args.inter + col) = pack8(db);
+      } else {
+        *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + col) = v;
       }
     }
   }
@@ -541,6 +558,7 @@ extern "C" int fmoe_gateup_fwd(const void* x_routed, const void* x_shared, const
   if (!offsets || !w1 || !w3 || !ab || !h || (rows_routed && !x_routed) ||
       (rows_shared && !x_shared))
     return FMOE_ERR_INVALID_ARG;
+  if (!aligned16(ab) || !aligned16(h)) return FMOE_ERR_ALIGN;
   GemmArgs a = {};
   a.a_routed = static_cast<const uint16_t*>(x_routed);
   a.a_shared = static_cast<const uint16_t*>(x_shared);
@@ -570,6 +588,7 @@ extern "C" int fmoe_down_fwd(const void* h, const int32_t* offsets, int n_expert
   if (st) return st;
   if (rows_routed + rows_shared == 0) return FMOE_OK;
   if (!h || !offsets || !w2 || !out) return FMOE_ERR_INVALID_ARG;
+  if (!aligned16(out)) return FMOE_ERR_ALIGN;
   GemmArgs a = {};
   a.a_routed = static_cast<const uint16_t*>(h);
   a.a_shared = nullptr;
@@ -591,14 +610,15 @@ extern "C" int fmoe_down_fwd(const void* h, const int32_t* offsets, int n_expert
 
 extern "C" int fmoe_down_bwd_dx(const void* d_out_routed, const void* d_out_shared,
                                 const int32_t* offsets, int n_experts, int64_t rows_routed,
-                                int64_t rows_shared, int64_t dim, int64_t inter,
-                                const void* const* w2, const void* ab, void* d_ab, void* stream) {
+                                int64_t rows_shared, int64_t dim, int64_t inter, const void* w2t,
+                                const void* ab, void* d_ab, void* stream) {
   int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
   if (st) return st;
   if (rows_routed + rows_shared == 0) return FMOE_OK;
-  if (!offsets || !w2 || !ab || !d_ab || (rows_routed && !d_out_routed) ||
+  if (!offsets || !w2t || !ab || !d_ab || (rows_routed && !d_out_routed) ||
       (rows_shared && !d_out_shared))
     return FMOE_ERR_INVALID_ARG;
+  if (!aligned16(w2t) || !aligned16(ab) || !aligned16(d_ab)) return FMOE_ERR_ALIGN;
   GemmArgs a = {};
   a.a_routed = static_cast<const uint16_t*>(d_out_routed);
   a.a_shared = static_cast<const uint16_t*>(d_out_shared);
@@ -607,27 +627,24 @@ extern "C" int fmoe_down_bwd_dx(const void* d_out_routed, const void* d_out_shar
   a.K = static_cast<int>(dim);
   a.N = static_cast<int>(inter);
   a.inter = static_cast<int>(inter);
-  a.ldb = inter;  // w2 is [dim, inter]: row k = dim index, columns = inter
+  a.ldb = dim;  // w2t[g] is [inter, dim]: row n = inter index, K = dim contiguous
   a.c0 = static_cast<uint16_t*>(d_ab);
   a.ldc0 = 2 * inter;
   a.aux = static_cast<const uint16_t*>(ab);
   a.ldaux = 2 * inter;
   const int G = n_experts + (rows_shared > 0 ? 1 : 0);
-  for (int g = 0; g < G; ++g) {
-    if (!w2[g]) return FMOE_ERR_INVALID_ARG;
-    a.b0[g] = static_cast<const uint16_t*>(w2[g]);
-  }
+  for (int g = 0; g < G; ++g) a.b0[g] = static_cast<const uint16_t*>(w2t) + static_cast<int64_t>(g) * inter * dim;
   return launch_rows<CfgRow, DOWN_BWD>(a, rows_routed, rows_shared, n_experts, stream);
 }
 
 extern "C" int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int n_experts,
                                   int64_t rows_routed, int64_t rows_shared, int64_t dim,
-                                  int64_t inter, const void* const* w1, const void* const* w3,
-                                  void* dx_rows, void* stream) {
+                                  int64_t inter, const void* w13t, void* dx_rows, void* stream) {
   int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
   if (st) return st;
   if (rows_routed + rows_shared == 0) return FMOE_OK;
-  if (!d_ab || !offsets || !w1 || !w3 || !dx_rows) return FMOE_ERR_INVALID_ARG;
+  if (!d_ab || !offsets || !w13t || !dx_rows) return FMOE_ERR_INVALID_ARG;
+  if (!aligned16(d_ab) || !aligned16(w13t) || !aligned16(dx_rows)) return FMOE_ERR_ALIGN;
   GemmArgs a = {};
   a.a_routed = static_cast<const uint16_t*>(d_ab);
   a.a_shared = nullptr;
@@ -636,15 +653,12 @@ extern "C" int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int 
   a.K = static_cast<int>(2 * inter);
   a.N = static_cast<int>(dim);
   a.inter = static_cast<int>(inter);
-  a.ldb = dim;  // w1, w3 are [inter, dim]: row k = inter index, columns = dim
+  a.ldb = 2 * inter;  // w13t[g] is [dim, 2*inter]: row n = dim index, K = 2*inter contiguous
   a.c0 = static_cast<uint16_t*>(dx_rows);
   a.ldc0 = dim;
   const int G = n_experts + (rows_shared > 0 ? 1 : 0);
-  for (int g = 0; g < G; ++g) {
-    if (!w1[g] || !w3[g]) return FMOE_ERR_INVALID_ARG;
-    a.b0[g] = static_cast<const uint16_t*>(w1[g]);
-    a.b1[g] = static_cast<const uint16_t*>(w3[g]);
-  }
+  for (int g = 0; g < G; ++g)
+    a.b0[g] = static_cast<const uint16_t*>(w13t) + static_cast<int64_t>(g) * dim * 2 * inter;
   return launch_rows<CfgRow, GATEUP_BWD>(a, rows_routed, rows_shared, n_experts, stream);
 }
 

@@ -129,22 +129,31 @@ __global__ __launch_bounds__(256) void router_dlogit_kernel(
 
 // Gate weight/bias gradient as a segmented column reduction over the
 // expert-contiguous rows:  dWg[e] = sum_{r in e} dl[perm[r]] * x_perm[r],
-// dbg[e] = sum_{r in e} dl[perm[r]].  Stage 1: each block reduces a chunk of
-// kChunkRows rows of one expert (chunk c of expert e covers rows
-// offsets[e] + c*kChunkRows ...) into partial[e][c][dim+1].  Stage 2 sums the
-// chunks of each expert in chunk order.  Both orders are fixed.
-constexpr int kChunkRows = 256;
+// dbg[e] = sum_{r in e} dl[perm[r]].  Expert e's rows are cut into
+// ceil(M_e / kChunkRows) chunks, numbered consecutively over the experts
+// (chunk_base(e) = sum of the chunk counts of experts < e).  Stage 1: one
+// block per chunk reduces its rows into partial[chunk][dim+1].  Stage 2 adds
+// the chunks of each expert in chunk order.  Both orders are fixed.
+constexpr int kChunkRows = 64;
 
-__global__ __launch_bounds__(256) void router_wgrad_partial_kernel(
+__device__ __forceinline__ int expert_chunks(const int32_t* offsets, int e) {
+  return (offsets[e + 1] - offsets[e] + kChunkRows - 1) / kChunkRows;
+}
+
+__global__ __launch_bounds__(128) void router_wgrad_partial_kernel(
     const float* __restrict__ dl, const int32_t* __restrict__ perm,
-    const int32_t* __restrict__ offsets, const uint16_t* __restrict__ x_perm, int dim,
-    int max_chunks, float* __restrict__ partial) {
-  const int e = blockIdx.y;
-  const int c = blockIdx.x;
+    const int32_t* __restrict__ offsets, int E, const uint16_t* __restrict__ x_perm, int dim,
+    float* __restrict__ partial) {
+  int c = blockIdx.x, e = 0;
+  for (; e < E; ++e) {
+    const int n = expert_chunks(offsets, e);
+    if (c < n) break;
+    c -= n;
+  }
+  if (e >= E) return;  // grid is an upper bound on the chunk count
   const int r0 = offsets[e] + c * kChunkRows;
   const int r1 = min(offsets[e + 1], r0 + kChunkRows);
-  float* out = partial + (static_cast<int64_t>(e) * max_chunks + c) * (dim + 1);
-  if (r0 >= offsets[e + 1]) return;  // chunk beyond this expert's rows
+  float* out = partial + static_cast<int64_t>(blockIdx.x) * (dim + 1);
   const int nchunk8 = dim / 8;
   for (int col8 = threadIdx.x; col8 <= nchunk8; col8 += blockDim.x) {
     if (col8 == nchunk8) {  // bias column
@@ -168,16 +177,16 @@ __global__ __launch_bounds__(256) void router_wgrad_partial_kernel(
 
 __global__ __launch_bounds__(256) void router_wgrad_final_kernel(
     const float* __restrict__ partial, const int32_t* __restrict__ offsets, int E, int dim,
-    int max_chunks, int grad_dtype, void* __restrict__ dwg, void* __restrict__ dbg) {
+    int grad_dtype, void* __restrict__ dwg, void* __restrict__ dbg) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;  // over E*(dim+1)
   if (i >= E * (dim + 1)) return;
   const int e = i / (dim + 1);
   const int col = i % (dim + 1);
-  const int rows = offsets[e + 1] - offsets[e];
-  const int nch = (rows + kChunkRows - 1) / kChunkRows;
+  int base = 0;
+  for (int q = 0; q < e; ++q) base += expert_chunks(offsets, q);
+  const int nch = expert_chunks(offsets, e);
   float acc = 0.0f;
-  for (int c = 0; c < nch; ++c)
-    acc = acc + partial[(static_cast<int64_t>(e) * max_chunks + c) * (dim + 1) + col];
+  for (int c = 0; c < nch; ++c) acc = acc + partial[static_cast<int64_t>(base + c) * (dim + 1) + col];
   if (col < dim) {
     const int64_t o = static_cast<int64_t>(e) * dim + col;
     if (grad_dtype == FMOE_BF16) static_cast<uint16_t*>(dwg)[o] = f2bf(acc);
@@ -229,11 +238,16 @@ extern "C" int fmoe_router_fwd(const void* x, const void* gate_w, const void* ga
   return launch_status();
 }
 
+namespace fmoe {
+// Upper bound of sum over experts of ceil(M_e / kChunkRows) with sum M_e = T*k.
+inline int64_t router_max_chunks(int64_t T, int n_experts, int k) {
+  return (T * k) / kChunkRows + n_experts;
+}
+}  // namespace fmoe
+
 extern "C" size_t fmoe_router_bwd_workspace_bytes(int64_t T, int64_t dim, int n_experts, int k) {
-  (void)k;
-  if (T <= 0 || dim <= 0 || n_experts <= 0) return 0;
-  const int64_t max_chunks = ceil_div(T, kChunkRows);  // an expert holds at most T rows
-  return static_cast<size_t>(n_experts) * max_chunks * (dim + 1) * sizeof(float);
+  if (T <= 0 || dim <= 0 || n_experts <= 0 || k <= 0) return 0;
+  return static_cast<size_t>(router_max_chunks(T, n_experts, k) * (dim + 1)) * sizeof(float);
 }
 
 extern "C" int fmoe_router_bwd(const float* d_weights, const float* topv, const int32_t* perm,
@@ -262,12 +276,12 @@ extern "C" int fmoe_router_bwd(const float* d_weights, const float* topv, const 
   if (!aligned16(x_perm)) return FMOE_ERR_ALIGN;
   router_dlogit_kernel<<<dim3(ceil_div(T, 256)), dim3(256), 0, s>>>(d_weights, topv, (int)T, k,
                                                                     route_scale, d_logits);
-  const int max_chunks = static_cast<int>(ceil_div(T, kChunkRows));
+  const int64_t max_chunks = router_max_chunks(T, n_experts, k);
   float* partial = static_cast<float*>(workspace);
-  router_wgrad_partial_kernel<<<dim3(max_chunks, n_experts), dim3(128), 0, s>>>(
-      d_logits, perm, offsets, static_cast<const uint16_t*>(x_perm), (int)dim, max_chunks, partial);
+  router_wgrad_partial_kernel<<<dim3(max_chunks), dim3(128), 0, s>>>(
+      d_logits, perm, offsets, n_experts, static_cast<const uint16_t*>(x_perm), (int)dim, partial);
   const int64_t n = static_cast<int64_t>(n_experts) * (dim + 1);
   router_wgrad_final_kernel<<<dim3(ceil_div(n, 256)), dim3(256), 0, s>>>(
-      partial, offsets, n_experts, (int)dim, max_chunks, grad_dtype, d_gate_w, d_gate_b);
+      partial, offsets, n_experts, (int)dim, grad_dtype, d_gate_w, d_gate_b);
   return launch_status();
 }

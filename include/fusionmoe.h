@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define FMOE_ABI_VERSION 1
+#define FMOE_ABI_VERSION 2
 #define FMOE_MAX_EXPERTS 64
 #define FMOE_MAX_TOPK 8
 
@@ -155,23 +155,31 @@ int fmoe_combine_bwd(const void* dy, int dy_dtype, const void* expert_out,
 
 /* ---------------------------------------------------------------------------
  * Backward of SwiGLUExpert (autograd of models/moe.py:21), grouped like the
- * forward.  fmoe_down_bwd_dx: dh = d_out w2 (bf16-rounded), then the SwiGLU
- * backward in the epilogue:  da = bf16(bf16(dh*b) * silu'(a)),
- * db = bf16(dh * bf16(silu(a))).  d_out_routed: [rows_routed, dim];
- * d_out_shared: [rows_shared, dim]; ab from fmoe_gateup_fwd; d_ab: [rows, 2*inter].
+ * forward.  The dX products multiply by the weights along their output
+ * dimension, so they read transposed copies made once per backward pass:
+ *   w2t  [G, inter, dim]       w2t[g]  = w2[g]^T
+ *   w13t [G, dim, 2*inter]     w13t[g] = [w1[g]; w3[g]]^T
+ * (G = routed experts + shared expert; caller-allocated, contiguous).
  * ------------------------------------------------------------------------- */
+int fmoe_transpose_weights(const void* const* w1, const void* const* w3,
+                           const void* const* w2, int n_groups, int64_t dim,
+                           int64_t inter, void* w13t, void* w2t, void* stream);
+
+/* dh = d_out w2 (bf16-rounded), then the SwiGLU backward in the epilogue:
+ *   da = bf16(bf16(dh*b) * silu'(a)),  db = bf16(dh * bf16(silu(a))).
+ * d_out_routed: [rows_routed, dim]; d_out_shared: [rows_shared, dim];
+ * ab from fmoe_gateup_fwd; d_ab: [rows, 2*inter]. */
 int fmoe_down_bwd_dx(const void* d_out_routed, const void* d_out_shared,
                      const int32_t* offsets, int n_experts,
                      int64_t rows_routed, int64_t rows_shared,
-                     int64_t dim, int64_t inter, const void* const* w2,
+                     int64_t dim, int64_t inter, const void* w2t,
                      const void* ab, void* d_ab, void* stream);
 
 /* dx_rows = da w1 + db w3 for every row (one product over K = 2*inter);
  * dx_rows: [rows, dim] bf16. */
 int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int n_experts,
                        int64_t rows_routed, int64_t rows_shared,
-                       int64_t dim, int64_t inter,
-                       const void* const* w1, const void* const* w3,
+                       int64_t dim, int64_t inter, const void* w13t,
                        void* dx_rows, void* stream);
 
 /* Grouped weight gradient, the dW half of nn.Linear backward for every expert:

@@ -145,8 +145,9 @@ def test_backward_products(gpu_device, counts, shared, d, I):
     w2 = [_bf(d, I, scale=0.05, g=g) for _ in range(G)]
     D = gpu_device
     dv = lambda ts: [t.to(D) for t in ts]
-    d_ab = K.down_bwd_dx(do_r.to(D), do_s.to(D) if shared else None, offsets, E, dv(w2), ab.to(D), I)
-    dx_rows = K.gateup_bwd_dx(d_ab, offsets, E, rows_r, shared, dv(w1), dv(w3), d)
+    w13t, w2t = K.transpose_weights(dv(w1), dv(w3), dv(w2))
+    d_ab = K.down_bwd_dx(do_r.to(D), do_s.to(D) if shared else None, offsets, E, w2t, ab.to(D), I)
+    dx_rows = K.gateup_bwd_dx(d_ab, offsets, E, rows_r, shared, w13t, d)
     dw2 = [torch.empty(d, I, dtype=torch.bfloat16, device=D) for _ in range(G)]
     K.weight_grad(do_r.to(D), do_s.to(D) if shared else None, h.to(D), None, offsets, E, rows_r, shared,
                   d, dw2, None, torch.bfloat16)
@@ -182,3 +183,17 @@ def test_backward_products(gpu_device, counts, shared, d, I):
         dw3_ref = dbg.T @ xs[r0:r1].float()
         assert rel_l2(dw1[grp].cpu(), dw1_ref) < 1e-5
         assert rel_l2(dw3[grp].cpu(), dw3_ref) < 1e-5
+
+
+@pytest.mark.parametrize("G,d,I", [(9, 768, 2048), (2, 64, 192), (3, 192, 64)])
+def test_transpose_weights_bit_exact(gpu_device, G, d, I):
+    g = torch.Generator().manual_seed(G)
+    w1 = [_bf(I, d, g=g) for _ in range(G)]
+    w3 = [_bf(I, d, g=g) for _ in range(G)]
+    w2 = [_bf(d, I, g=g) for _ in range(G)]
+    dv = lambda ts: [t.to(gpu_device) for t in ts]
+    w13t, w2t = K.transpose_weights(dv(w1), dv(w3), dv(w2))
+    want13 = torch.stack([torch.cat([a, b]).T for a, b in zip(w1, w3)])
+    want2 = torch.stack([w.T for w in w2])
+    assert torch.equal(w13t.cpu().view(torch.int16), want13.contiguous().view(torch.int16))
+    assert torch.equal(w2t.cpu().view(torch.int16), want2.contiguous().view(torch.int16))

@@ -21,7 +21,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     syms = declared_symbols()
-    assert len(syms) == 16
+    assert len(syms) == 17
     for s in syms:
         assert hasattr(lib, s), s
     assert set(syms) == set(_lib.SIGNATURES), "ctypes binding and header disagree"
@@ -53,7 +53,7 @@ def test_argument_errors_without_gpu():
     # size queries
     assert lib.fmoe_dispatch_workspace_bytes(16384, 8, 2) == 2 * 32 * 8 * 4
     assert lib.fmoe_weight_grad_workspace_bytes(32768, 16384, 8, 768, 2048) > 0
-    assert lib.fmoe_router_bwd_workspace_bytes(16384, 768, 8, 2) == 8 * 64 * 769 * 4
+    assert lib.fmoe_router_bwd_workspace_bytes(16384, 768, 8, 2) == (16384 * 2 // 64 + 8) * 769 * 4
 
 
 def test_parameter_names_shapes_and_count():
