@@ -44,7 +44,10 @@ def _timed(fn):
 
 
 def _stream() -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    # The raw current-stream handle of the current device (what
+    # torch.cuda.current_stream().cuda_stream returns, without building a
+    # Stream object: that costs more than a kernel launch on small batches).
+    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(torch._C._cuda_getDevice()))
 
 
 def _req(t: torch.Tensor, name: str, dtype: torch.dtype | None = None) -> int:

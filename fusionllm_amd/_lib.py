@@ -98,9 +98,20 @@ def check(rc: int, what: str) -> None:
         raise FusionMoEError(f"{what} failed: {msg} (status {rc})")
 
 
+_PTR_CACHE: dict = {}
+
+
 def ptr_array(ptrs) -> ctypes.Array:
-    """Host array of device pointers for the per-expert weight arguments."""
-    arr = (c_void_p * len(ptrs))()
-    for i, p in enumerate(ptrs):
-        arr[i] = p
+    """Host array of device pointers for the per-expert weight arguments.
+
+    The arrays are read-only inputs of the C entry points, so one array per
+    distinct pointer tuple is kept and reused (the weights of a module keep
+    their storage from step to step)."""
+    key = tuple(ptrs)
+    arr = _PTR_CACHE.get(key)
+    if arr is None:
+        if len(_PTR_CACHE) > 4096:
+            _PTR_CACHE.clear()
+        arr = (c_void_p * len(key))(*key)
+        _PTR_CACHE[key] = arr
     return arr

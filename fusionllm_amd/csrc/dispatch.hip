@@ -44,22 +44,36 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_hist_kernel(
     block_hist[static_cast<int64_t>(blockIdx.x) * E + e] = cnt[e];
 }
 
-// One workgroup.  block_base[b][e] = offsets[e] + sum_{b' < b} block_hist[b'][e].
-__global__ __launch_bounds__(64) void dispatch_scan_kernel(
+// One workgroup of 16 waves; wave w scans experts w, w + 16, ...
+// block_base[b][e] = offsets[e] + sum_{b' < b} block_hist[b'][e]: pass 1 adds
+// each expert's block counts (wave reduction), thread 0 turns the totals into
+// offsets, pass 2 writes the per-block bases with a 64-lane inclusive scan
+// (shfl_up) per chunk of 64 blocks, carried across chunks.  Integer sums, so
+// the order does not change the result.
+constexpr int kScanThreads = 1024;
+
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int u = __shfl_up(v, off, 64);
+    if (lane >= off) v += u;
+  }
+  return v;
+}
+
+__global__ __launch_bounds__(kScanThreads) void dispatch_scan_kernel(
     const int32_t* __restrict__ block_hist, int nblocks, int E, int32_t* __restrict__ block_base,
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets) {
   __shared__ int total[FMOE_MAX_EXPERTS];
   __shared__ int start[FMOE_MAX_EXPERTS + 1];
-  const int e = threadIdx.x;
-  if (e < E) {
-    int run = 0;
-    for (int b = 0; b < nblocks; ++b) {
-      const int64_t o = static_cast<int64_t>(b) * E + e;
-      const int h = block_hist[o];
-      block_base[o] = run;
-      run += h;
-    }
-    total[e] = run;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int nwaves = kScanThreads / 64;
+  for (int e = wave; e < E; e += nwaves) {
+    int sum = 0;
+    for (int b = lane; b < nblocks; b += 64) sum += block_hist[static_cast<int64_t>(b) * E + e];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    if (lane == 0) total[e] = sum;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -68,12 +82,22 @@ __global__ __launch_bounds__(64) void dispatch_scan_kernel(
     start[E] = run;
   }
   __syncthreads();
-  if (e < E) {
+  for (int e = threadIdx.x; e < E; e += kScanThreads) {
     counts[e] = total[e];
     offsets[e] = start[e];
-    for (int b = 0; b < nblocks; ++b) block_base[static_cast<int64_t>(b) * E + e] += start[e];
   }
-  if (e == 0) offsets[E] = start[E];
+  if (threadIdx.x == 0) offsets[E] = start[E];
+  for (int e = wave; e < E; e += nwaves) {
+    int carry = start[e];
+    for (int b0 = 0; b0 < nblocks; b0 += 64) {
+      const int b = b0 + lane;
+      const int64_t o = static_cast<int64_t>(b) * E + e;
+      const int h = b < nblocks ? block_hist[o] : 0;
+      const int incl = wave_incl_scan(h, lane);
+      if (b < nblocks) block_base[o] = carry + incl - h;
+      carry += __shfl(incl, 63, 64);
+    }
+  }
 }
 
 __global__ __launch_bounds__(kDispThreads) void dispatch_scatter_kernel(
@@ -160,7 +184,7 @@ extern "C" int fmoe_dispatch(const int32_t* idx, const void* x, int64_t T, int64
   const int64_t nblocks = ceil_div(n_slots, kSlotsPerBlock);
   if (T == 0) {
     // Empty batch: every count and offset is zero (scan over zero blocks).
-    dispatch_scan_kernel<<<1, 64, 0, s>>>(nullptr, 0, n_experts, nullptr, counts, offsets);
+    dispatch_scan_kernel<<<1, kScanThreads, 0, s>>>(nullptr, 0, n_experts, nullptr, counts, offsets);
     return launch_status();
   }
   if (!idx || !x || !perm || !pos_of_slot || !workspace) return FMOE_ERR_INVALID_ARG;
@@ -170,8 +194,8 @@ extern "C" int fmoe_dispatch(const int32_t* idx, const void* x, int64_t T, int64
   int32_t* block_base = block_hist + nblocks * n_experts;
   dispatch_hist_kernel<<<dim3(nblocks), dim3(kDispThreads), 0, s>>>(idx, (int)n_slots, n_experts,
                                                                    block_hist);
-  dispatch_scan_kernel<<<1, 64, 0, s>>>(block_hist, (int)nblocks, n_experts, block_base, counts,
-                                        offsets);
+  dispatch_scan_kernel<<<1, kScanThreads, 0, s>>>(block_hist, (int)nblocks, n_experts, block_base,
+                                                  counts, offsets);
   dispatch_scatter_kernel<<<dim3(nblocks), dim3(kDispThreads), 0, s>>>(
       idx, (int)n_slots, n_experts, block_base, perm, pos_of_slot);
   if (x_perm) {

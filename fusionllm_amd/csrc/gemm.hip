@@ -170,6 +170,7 @@ struct GemmArgs {
   int64_t ldc0, ldc1, ldaux;
   const uint16_t* b0[FMOE_MAX_EXPERTS + 1];  // w1 / w2 / w2t / w13t
   const uint16_t* b1[FMOE_MAX_EXPERTS + 1];  // w3 (GATEUP_FWD only)
+  int small_max;  // groups with 1 .. small_max rows go to small_gemm_kernel (0: none)
 };
 
 // Epilogue staging: the tile's bf16 values in LDS, row-major with 512 bytes
@@ -205,7 +206,7 @@ __global__ __launch_bounds__(C::NT) void grouped_gemm_kernel(const GemmArgs args
       row_base = args.rows_routed;
       M = args.rows_shared;
     }
-    const int nt = ((M + C::BM - 1) / C::BM) * tiles_n;
+    const int nt = (M <= args.small_max) ? 0 : ((M + C::BM - 1) / C::BM) * tiles_n;
     if (tile < nt) break;
     tile -= nt;
   }
@@ -353,6 +354,114 @@ __global__ __launch_bounds__(C::NT) void grouped_gemm_kernel(const GemmArgs args
   }
 }
 
+// ---- small groups (decode-sized batches) -------------------------------------
+// A group of at most kSmallM rows would leave a 256 x 256 tile nearly empty
+// and run its whole K loop in one workgroup.  Here one workgroup owns a block
+// of 32 output columns of one group (GATEUP_FWD: 16 h columns, i.e. 16 rows
+// of w1 and the same 16 rows of w3), its 4 waves split K in four, stream
+// their MFMA fragments straight from memory (the weights are read once), and
+// the four partial tiles are added in wave order through LDS.
+constexpr int kSmallM = 128;
+constexpr int kSmallMB = kSmallM / 32;
+constexpr int kSmallUnroll = 4;
+
+template <int MODE>
+__global__ __launch_bounds__(256) void small_gemm_kernel(const GemmArgs args) {
+  static_assert(MODE == GATEUP_FWD || MODE == DOWN_FWD, "forward products only");
+  __shared__ float red[4][kSmallMB][16][64];  // [wave][m block][register][lane]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ncb = (MODE == GATEUP_FWD) ? args.N / 16 : args.N / 32;
+  const int g = blockIdx.x / ncb, cb = blockIdx.x % ncb;
+  int row_base, M;
+  if (g < args.E) {
+    row_base = args.offsets[g];
+    M = args.offsets[g + 1] - row_base;
+  } else {
+    row_base = args.rows_routed;
+    M = args.rows_shared;
+  }
+  if (M == 0 || M > args.small_max) return;
+  const uint16_t* A = (g < args.E || args.a_shared == nullptr)
+                          ? args.a_routed + static_cast<int64_t>(row_base) * args.lda
+                          : args.a_shared;
+  // B fragment column j = lane % 32: the weight row this lane streams
+  const int j = lane & 31, kh = (lane >> 5) * 8;
+  const uint16_t* wrow;
+  if constexpr (MODE == GATEUP_FWD)
+    wrow = (j < 16 ? args.b0[g] : args.b1[g]) + static_cast<int64_t>(cb * 16 + (j & 15)) * args.ldb;
+  else
+    wrow = args.b0[g] + static_cast<int64_t>(cb * 32 + j) * args.ldb;
+  const int mb_n = (M + 31) / 32;  // 1 .. kSmallMB
+  const uint16_t* ap[kSmallMB];
+#pragma unroll
+  for (int mb = 0; mb < kSmallMB; ++mb) {
+    const int r = min(32 * mb + j, M - 1);  // rows past M repeat the last row
+    ap[mb] = A + static_cast<int64_t>(r) * args.lda + kh;
+  }
+  const int kq = args.K / 4;  // a multiple of 16
+  const int k_begin = wave * kq, k_end = k_begin + kq;
+
+  f32x16 acc[kSmallMB];
+#pragma unroll
+  for (int mb = 0; mb < kSmallMB; ++mb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[mb][r] = 0.0f;
+  for (int k0 = k_begin; k0 < k_end; k0 += 16 * kSmallUnroll) {
+    bf16x8 bf[kSmallUnroll], af[kSmallUnroll][kSmallMB];
+#pragma unroll
+    for (int u = 0; u < kSmallUnroll; ++u) {
+      const int kk = k0 + 16 * u;
+      if (kk < k_end) {
+        bf[u] = *reinterpret_cast<const bf16x8*>(wrow + kk + kh);
+#pragma unroll
+        for (int mb = 0; mb < kSmallMB; ++mb)
+          if (mb < mb_n) af[u][mb] = *reinterpret_cast<const bf16x8*>(ap[mb] + kk);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kSmallUnroll; ++u) {
+      if (k0 + 16 * u < k_end) {
+#pragma unroll
+        for (int mb = 0; mb < kSmallMB; ++mb)
+          if (mb < mb_n) acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[u][mb], bf[u], acc[mb], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int mb = 0; mb < kSmallMB; ++mb)
+    if (mb < mb_n)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[wave][mb][r][lane] = acc[mb][r];
+  __syncthreads();
+  // wave w finishes m blocks w, w + 4, ...: the four partials in wave order
+  for (int mb = wave; mb < mb_n; mb += 4) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float v = red[0][mb][r][lane];
+      v = v + red[1][mb][r][lane];
+      v = v + red[2][mb][r][lane];
+      v = v + red[3][mb][r][lane];
+      // lane holds C[m = 32 mb + 8 (r / 4) + 4 (lane / 32) + r % 4][n = lane % 32]
+      const int m = 32 * mb + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      const int64_t row = row_base + m;
+      if constexpr (MODE == GATEUP_FWD) {
+        // lanes j < 16 hold a, lanes j + 16 hold b for the same h column
+        const float a = bf_round(v);
+        const float b = __shfl(a, (lane & 32) + (j & 15) + 16, 64);
+        if (m < M && j < 16) {
+          const int col = cb * 16 + j;
+          const float sv = bf_round(a * fast_sigmoid(a));
+          args.c0[row * args.ldc0 + col] = f2bf(a);
+          args.c0[row * args.ldc0 + args.inter + col] = f2bf(b);
+          args.c1[row * args.ldc1 + col] = f2bf(sv * b);
+        }
+      } else {
+        if (m < M) args.c0[row * args.ldc0 + cb * 32 + j] = f2bf(v);
+      }
+    }
+  }
+}
+
 // ---- weight gradients (K-grouped) -------------------------------------------
 // G_e = A_e^T B_e with A_e [M_e, m_out], B_e [M_e, n_out] (both MN-contiguous).
 // Work unit = (group, K chunk of kc rows, output tile).  A group whose rows fit
@@ -491,6 +600,8 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(const WgradArgs args) {
   }
 }
 
+// Adds the chunk partials of each multi-chunk group in chunk order; 8
+// consecutive outputs per thread (m_out * n_out is a multiple of 64).
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const WgradArgs args) {
   const int g = blockIdx.y;
   int row_base, M;
@@ -505,12 +616,18 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const WgradArgs args)
     if (cq > 1) pbase += cq;
   }
   const int64_t mn = static_cast<int64_t>(args.m_out) * args.n_out;
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= mn) return;
-  float acc = 0.0f;
-  for (int c = 0; c < chunks; ++c) acc = acc + args.partial[(pbase + c) * mn + i];
-  const int m = static_cast<int>(i / args.n_out), n = static_cast<int>(i % args.n_out);
-  store_grad(args, g, m, n, acc);
+  const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+  if (i0 >= mn) return;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int c = 0; c < chunks; ++c) {
+    const float4* src = reinterpret_cast<const float4*>(args.partial + (pbase + c) * mn + i0);
+    const float4 u = src[0], v = src[1];
+    acc[0] = acc[0] + u.x; acc[1] = acc[1] + u.y; acc[2] = acc[2] + u.z; acc[3] = acc[3] + u.w;
+    acc[4] = acc[4] + v.x; acc[5] = acc[5] + v.y; acc[6] = acc[6] + v.z; acc[7] = acc[7] + v.w;
+  }
+  const int m = static_cast<int>(i0 / args.n_out), n = static_cast<int>(i0 % args.n_out);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) store_grad(args, g, m, n + e, acc[e]);
 }
 
 // ---- host side --------------------------------------------------------------
@@ -525,15 +642,29 @@ int check_common(int n_experts, int64_t rows_routed, int64_t rows_shared, int64_
   return FMOE_OK;
 }
 
+// Row counts up to which a launch sends groups of <= kSmallM rows to the
+// small-group kernel (decode-sized batches); larger launches use the tiled
+// kernel for every group.
+constexpr int64_t kSmallLaunchRows = 4096;
+
 template <class C, int MODE>
 int launch_rows(GemmArgs& a, int64_t rows_routed, int64_t rows_shared, int E, void* stream) {
   constexpr int TN_COLS = (MODE == GATEUP_FWD) ? C::BN / 2 : C::BN;
   const int64_t tiles_n = ceil_div(a.N, TN_COLS);
+  constexpr bool kHasSmall = (MODE == GATEUP_FWD || MODE == DOWN_FWD);
+  a.small_max = (kHasSmall && rows_routed + rows_shared <= kSmallLaunchRows) ? kSmallM : 0;
   // Upper bound of sum over groups of ceil(M_g / BM): floor(rows/BM) + groups.
   const int64_t mt = rows_routed / C::BM + E + ceil_div(rows_shared, C::BM);
   const int64_t grid = mt * tiles_n;
   if (grid <= 0) return FMOE_OK;
   grouped_gemm_kernel<C, MODE><<<dim3(grid), dim3(C::NT), 0, as_stream(stream)>>>(a);
+  if constexpr (kHasSmall) {
+    if (a.small_max > 0) {
+      const int G = E + (rows_shared > 0 ? 1 : 0);
+      const int64_t ncb = (MODE == GATEUP_FWD) ? a.N / 16 : a.N / 32;
+      small_gemm_kernel<MODE><<<dim3(G * ncb), dim3(256), 0, as_stream(stream)>>>(a);
+    }
+  }
   return launch_status();
 }
 
@@ -663,19 +794,23 @@ extern "C" int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int 
 }
 
 namespace fmoe {
-// Rows per K chunk of the weight gradient: a multiple of 64 chosen so that the
-// largest possible group (all rows) splits into about 4 chunks.
-int64_t wgrad_kc(int64_t rows_routed, int64_t rows_shared) {
-  const int64_t rows = rows_routed > rows_shared ? rows_routed : rows_shared;
-  int64_t kc = ceil_div(ceil_div(rows, 4), 64) * 64;
-  return kc < 1024 ? 1024 : kc;
+// Rows per K chunk of the weight gradient.  A work unit is (group, chunk,
+// output tile); the chunk is sized so that the largest unit is about half of
+// one CU's average share (tiles * rows / 64 K-steps over 256 CUs), which keeps
+// the skewed groups (one or two experts holding most rows) from leaving a long
+// tail.  A multiple of 64, at least 256 rows.
+int64_t wgrad_kc(int64_t rows_routed, int64_t rows_shared, int64_t m_out, int64_t n_out) {
+  const int64_t rows = rows_routed + rows_shared;
+  const int64_t tiles = ceil_div(m_out, 256) * ceil_div(n_out, 256);
+  int64_t kc = (tiles * rows / 512) / 64 * 64;
+  return kc < 256 ? 256 : kc;
 }
 }  // namespace fmoe
 
 extern "C" size_t fmoe_weight_grad_workspace_bytes(int64_t rows_routed, int64_t rows_shared,
                                                    int n_experts, int64_t m_out, int64_t n_out) {
   if (rows_routed < 0 || rows_shared < 0 || n_experts <= 0 || m_out <= 0 || n_out <= 0) return 0;
-  const int64_t kc = wgrad_kc(rows_routed, rows_shared);
+  const int64_t kc = wgrad_kc(rows_routed, rows_shared, m_out, n_out);
   // sum over groups of ceil(M_g / kc) <= floor(rows / kc) + groups
   const int64_t chunks = (rows_routed + rows_shared) / kc + n_experts + 1;
   return static_cast<size_t>(chunks * m_out * n_out) * sizeof(float);
@@ -712,7 +847,7 @@ extern "C" int fmoe_weight_grad(const void* a_routed, const void* a_shared, int6
   a.m_out = static_cast<int>(m_out);
   a.n_out = static_cast<int>(n_out);
   a.m_split = static_cast<int>(m_split);
-  a.kc = static_cast<int>(wgrad_kc(rows_routed, rows_shared));
+  a.kc = static_cast<int>(wgrad_kc(rows_routed, rows_shared, m_out, n_out));
   a.out_dtype = out_dtype;
   a.partial = static_cast<float*>(workspace);
   const int G = n_experts + (rows_shared > 0 ? 1 : 0);
@@ -727,6 +862,6 @@ extern "C" int fmoe_weight_grad(const void* a_routed, const void* a_shared, int6
   hipStream_t s = as_stream(stream);
   wgrad_kernel<C><<<dim3(max_chunks * tiles), dim3(C::NT), 0, s>>>(a);
   const int64_t mn = m_out * n_out;
-  wgrad_reduce_kernel<<<dim3(ceil_div(mn, 256), G), dim3(256), 0, s>>>(a);
+  wgrad_reduce_kernel<<<dim3(ceil_div(mn, 256 * 8), G), dim3(256), 0, s>>>(a);
   return launch_status();
 }

@@ -5,6 +5,7 @@
 // weight/bias gradient.
 //
 // Logit summation order (reproduced exactly by oracle/router_ref.c):
+//   (dim <= 2048: the forward keeps a token's x chunks in registers)
 //   16 lanes cooperate on one token.  dim is cut into 8-element chunks;
 //   lane j owns chunks j, j+16, j+32, ... and accumulates, chunk by chunk and
 //   element by element in ascending order, acc = fmaf(x, w, acc) from 0.
@@ -16,49 +17,81 @@
 namespace fmoe {
 
 constexpr int kRouterLanes = 16;
+constexpr int kRouterTok = 32;       // tokens per workgroup (32 x 16 lanes = 512 threads)
+constexpr int kRouterEBlk = 16;      // experts whose gate rows sit in LDS at a time
+constexpr int kRouterMaxDim = 2048;  // a lane keeps its <= 16 x chunks in registers
 
-template <int EB>
-__global__ __launch_bounds__(256) void router_fwd_kernel(
+// One workgroup routes 32 tokens.  The gate rows are staged in LDS, 16
+// experts at a time, so the gate matrix is read from memory once per 32
+// tokens instead of once per token; each lane keeps its x chunks in
+// registers across the expert blocks.  The logits (without bias) go to LDS
+// and every lane of a token's group then computes the scores and the top-k.
+template <int EB, int NQ>  // NQ: x chunks per lane, NQ * 16 * 8 >= dim
+__global__ __launch_bounds__(512) void router_fwd_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg,
     const uint16_t* __restrict__ bg, int T, int dim, int E, int k, float route_scale,
     int32_t* __restrict__ idx, int64_t* __restrict__ idx64, float* __restrict__ wout,
     float* __restrict__ vout) {
+  __shared__ __attribute__((aligned(16))) uint4 wsh[kRouterEBlk * NQ * kRouterLanes];
+  __shared__ float lsh[kRouterTok * EB];
   const int lane16 = threadIdx.x % kRouterLanes;
-  const int t = (blockIdx.x * blockDim.x + threadIdx.x) / kRouterLanes;
+  const int tl = threadIdx.x / kRouterLanes;
+  const int t = blockIdx.x * kRouterTok + tl;
   const bool active = t < T;
-  const int tc = active ? t : T - 1;  // keep all lanes in the shuffles
-
-  float acc[EB];
-#pragma unroll
-  for (int e = 0; e < EB; ++e) acc[e] = 0.0f;
-
+  const int tc = active ? t : T - 1;  // idle lanes route a copy of the last token
   const int nchunk = dim / 8;
+
   const uint4* xrow = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(tc) * dim);
-  for (int c = lane16; c < nchunk; c += kRouterLanes) {
-    float xf[8];
-    unpack8(xrow[c], xf);
+  uint4 xr[NQ];
 #pragma unroll
-    for (int e = 0; e < EB; ++e) {
-      if (e < E) {
-        const uint4 wv = reinterpret_cast<const uint4*>(wg + static_cast<int64_t>(e) * dim)[c];
-        float wf[8];
-        unpack8(wv, wf);
+  for (int q = 0; q < NQ; ++q) {
+    const int c = lane16 + kRouterLanes * q;
+    xr[q] = c < nchunk ? xrow[c] : make_uint4(0, 0, 0, 0);
+  }
+
+  for (int e0 = 0; e0 < E; e0 += kRouterEBlk) {
+    const int ne = min(kRouterEBlk, E - e0);
+    __syncthreads();  // the previous block's gate rows are no longer read
+    for (int i = threadIdx.x; i < ne * nchunk; i += blockDim.x)
+      wsh[i] = reinterpret_cast<const uint4*>(wg + static_cast<int64_t>(e0) * dim)[i];
+    __syncthreads();
+    float acc[kRouterEBlk];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[e] = fmaf(xf[i], wf[i], acc[e]);
+    for (int e = 0; e < kRouterEBlk; ++e) acc[e] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int c = lane16 + kRouterLanes * q;
+      if (c < nchunk) {
+        float xf[8];
+        unpack8(xr[q], xf);
+#pragma unroll
+        for (int e = 0; e < kRouterEBlk; ++e) {
+          if (e < ne) {
+            float wf[8];
+            unpack8(wsh[e * nchunk + c], wf);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[e] = fmaf(xf[i], wf[i], acc[e]);
+          }
+        }
       }
     }
-  }
 #pragma unroll
-  for (int off = kRouterLanes / 2; off >= 1; off >>= 1) {
+    for (int off = kRouterLanes / 2; off >= 1; off >>= 1) {
 #pragma unroll
-    for (int e = 0; e < EB; ++e) acc[e] = acc[e] + __shfl_xor(acc[e], off, kRouterLanes);
+      for (int e = 0; e < kRouterEBlk; ++e) acc[e] = acc[e] + __shfl_xor(acc[e], off, kRouterLanes);
+    }
+    // every lane now holds the block's logits; lane e writes expert e0 + e
+#pragma unroll
+    for (int e = 0; e < kRouterEBlk; ++e)
+      if (e == lane16 && e < ne) lsh[tl * EB + e0 + e] = acc[e];
   }
+  __syncthreads();
 
-  // Every lane of the group now holds all logits; scores and top-k are
-  // computed redundantly and lane j < k writes the j-th choice.
+  // Scores and top-k, computed redundantly by the 16 lanes of a token;
+  // lane j < k writes the j-th choice.
   float s[EB];
 #pragma unroll
-  for (int e = 0; e < EB; ++e) s[e] = (e < E) ? fm_sigmoid(acc[e] + bf2f(bg[e])) : 0.0f;
+  for (int e = 0; e < EB; ++e) s[e] = (e < E) ? fm_sigmoid(lsh[tl * EB + e] + bf2f(bg[e])) : 0.0f;
 
   uint64_t taken = 0;
   int sel[FMOE_MAX_TOPK];
@@ -175,25 +208,34 @@ __global__ __launch_bounds__(128) void router_wgrad_partial_kernel(
   }
 }
 
+// One block per (16 columns, expert): 16 chunk lanes per column each add the
+// chunks c = lane, lane + 16, ... in order; the 16 lane sums are then added
+// in lane order.  Fixed order, so deterministic.
 __global__ __launch_bounds__(256) void router_wgrad_final_kernel(
     const float* __restrict__ partial, const int32_t* __restrict__ offsets, int E, int dim,
     int grad_dtype, void* __restrict__ dwg, void* __restrict__ dbg) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;  // over E*(dim+1)
-  if (i >= E * (dim + 1)) return;
-  const int e = i / (dim + 1);
-  const int col = i % (dim + 1);
+  __shared__ float lsum[16][17];
+  const int e = blockIdx.y;
+  const int cl = threadIdx.x & 15, lanec = threadIdx.x >> 4;
+  const int col = blockIdx.x * 16 + cl;
   int base = 0;
   for (int q = 0; q < e; ++q) base += expert_chunks(offsets, q);
   const int nch = expert_chunks(offsets, e);
   float acc = 0.0f;
-  for (int c = 0; c < nch; ++c) acc = acc + partial[static_cast<int64_t>(base + c) * (dim + 1) + col];
+  if (col <= dim)
+    for (int c = lanec; c < nch; c += 16) acc = acc + partial[static_cast<int64_t>(base + c) * (dim + 1) + col];
+  lsum[lanec][cl] = acc;
+  __syncthreads();
+  if (lanec != 0 || col > dim) return;
+  float tot = lsum[0][cl];
+  for (int l = 1; l < 16; ++l) tot = tot + lsum[l][cl];
   if (col < dim) {
     const int64_t o = static_cast<int64_t>(e) * dim + col;
-    if (grad_dtype == FMOE_BF16) static_cast<uint16_t*>(dwg)[o] = f2bf(acc);
-    else static_cast<float*>(dwg)[o] = acc;
+    if (grad_dtype == FMOE_BF16) static_cast<uint16_t*>(dwg)[o] = f2bf(tot);
+    else static_cast<float*>(dwg)[o] = tot;
   } else {
-    if (grad_dtype == FMOE_BF16) static_cast<uint16_t*>(dbg)[e] = f2bf(acc);
-    else static_cast<float*>(dbg)[e] = acc;
+    if (grad_dtype == FMOE_BF16) static_cast<uint16_t*>(dbg)[e] = f2bf(tot);
+    else static_cast<float*>(dbg)[e] = tot;
   }
 }
 
@@ -216,24 +258,32 @@ extern "C" int fmoe_router_fwd(const void* x, const void* gate_w, const void* ga
                                int64_t* idx64, float* weights, float* topv, void* stream) {
   if (T < 0 || dim <= 0) return FMOE_ERR_INVALID_ARG;
   if (n_experts <= 0 || n_experts > FMOE_MAX_EXPERTS) return FMOE_ERR_TOO_MANY_EXPERTS;
-  if (k <= 0 || k > FMOE_MAX_TOPK || k > n_experts || dim % 64 != 0) return FMOE_ERR_SHAPE;
+  if (k <= 0 || k > FMOE_MAX_TOPK || k > n_experts || dim % 64 != 0 || dim > kRouterMaxDim)
+    return FMOE_ERR_SHAPE;
   if (T == 0) return FMOE_OK;
   if (!x || !gate_w || !gate_b || !idx || !weights || !topv) return FMOE_ERR_INVALID_ARG;
   if (!aligned16(x) || !aligned16(gate_w)) return FMOE_ERR_ALIGN;
-  const int threads = 256;
-  const int64_t blocks = ceil_div(T * kRouterLanes, threads);
+  const int threads = kRouterTok * kRouterLanes;
+  const int64_t blocks = ceil_div(T, kRouterTok);
   hipStream_t s = as_stream(stream);
   auto xs = static_cast<const uint16_t*>(x);
   auto ws = static_cast<const uint16_t*>(gate_w);
   auto bs = static_cast<const uint16_t*>(gate_b);
-#define FMOE_ROUTER_LAUNCH(EB)                                                                  \
-  router_fwd_kernel<EB><<<dim3(blocks), dim3(threads), 0, s>>>(xs, ws, bs, (int)T, (int)dim,    \
-                                                               n_experts, k, route_scale, idx,  \
-                                                               idx64, weights, topv)
-  if (n_experts <= 8) FMOE_ROUTER_LAUNCH(8);
-  else if (n_experts <= 16) FMOE_ROUTER_LAUNCH(16);
-  else if (n_experts <= 32) FMOE_ROUTER_LAUNCH(32);
-  else FMOE_ROUTER_LAUNCH(64);
+#define FMOE_ROUTER_LAUNCH(EB, NQ)                                                               \
+  router_fwd_kernel<EB, NQ><<<dim3(blocks), dim3(threads), 0, s>>>(xs, ws, bs, (int)T, (int)dim, \
+                                                                   n_experts, k, route_scale,   \
+                                                                   idx, idx64, weights, topv)
+#define FMOE_ROUTER_LAUNCH_E(NQ)                 \
+  do {                                           \
+    if (n_experts <= 8) FMOE_ROUTER_LAUNCH(8, NQ);       \
+    else if (n_experts <= 16) FMOE_ROUTER_LAUNCH(16, NQ); \
+    else if (n_experts <= 32) FMOE_ROUTER_LAUNCH(32, NQ); \
+    else FMOE_ROUTER_LAUNCH(64, NQ);                      \
+  } while (0)
+  if (dim <= 512) FMOE_ROUTER_LAUNCH_E(4);
+  else if (dim <= 1024) FMOE_ROUTER_LAUNCH_E(8);
+  else FMOE_ROUTER_LAUNCH_E(16);
+#undef FMOE_ROUTER_LAUNCH_E
 #undef FMOE_ROUTER_LAUNCH
   return launch_status();
 }
@@ -280,8 +330,7 @@ extern "C" int fmoe_router_bwd(const float* d_weights, const float* topv, const 
   float* partial = static_cast<float*>(workspace);
   router_wgrad_partial_kernel<<<dim3(max_chunks), dim3(128), 0, s>>>(
       d_logits, perm, offsets, n_experts, static_cast<const uint16_t*>(x_perm), (int)dim, partial);
-  const int64_t n = static_cast<int64_t>(n_experts) * (dim + 1);
-  router_wgrad_final_kernel<<<dim3(ceil_div(n, 256)), dim3(256), 0, s>>>(
+  router_wgrad_final_kernel<<<dim3(ceil_div(dim + 1, 16), n_experts), dim3(256), 0, s>>>(
       partial, offsets, n_experts, (int)dim, grad_dtype, d_gate_w, d_gate_b);
   return launch_status();
 }

@@ -26,6 +26,8 @@ gradients come back in each parameter's own dtype.
 """
 from __future__ import annotations
 
+import contextlib
+
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
@@ -50,6 +52,26 @@ def _as_bf16(t: torch.Tensor) -> torch.Tensor:
     return t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)
 
 
+def _forward_pass(meta, x, gate_w, gate_b, weights):
+    """The forward kernels of DeepSeekMoE.forward (models/moe.py:79-87); returns
+    the output and every intermediate the backward pass needs."""
+    E, k, inter, rs, has_shared, out_dtype = meta
+    T, d = x.shape
+    xb = _as_bf16(x).contiguous()
+    gwb, gbb = _as_bf16(gate_w).contiguous(), _as_bf16(gate_b).contiguous()
+    wb = [_as_bf16(w).contiguous() for w in weights]
+    G = E + (1 if has_shared else 0)
+    w1s, w3s, w2s = wb[0::3][:G], wb[1::3][:G], wb[2::3][:G]
+
+    idx, idx64, w, v = K.router_fwd(xb, gwb, gbb, k, rs)
+    counts, offsets, perm, pos, x_perm = K.dispatch(idx, xb, E)
+    rows_r, rows_s = T * k, (T if has_shared else 0)
+    ab, h = K.gateup_fwd(x_perm, xb if has_shared else None, offsets, E, w1s, w3s, inter)
+    o = K.down_fwd(h, offsets, E, rows_r, rows_s, w2s, d)
+    y = K.combine_fwd(o, idx, w, pos, rows_r, has_shared, out_dtype)
+    return xb, gwb, wb, idx, idx64, w, v, counts, offsets, perm, pos, x_perm, ab, h, o, y
+
+
 class _MoEBlockFunction(torch.autograd.Function):
     """Forward and backward of DeepSeekMoE.forward (models/moe.py:79-87) on the kernels.
 
@@ -62,19 +84,8 @@ class _MoEBlockFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, meta, x, gate_w, gate_b, *weights):
         E, k, inter, rs, has_shared, out_dtype = meta
-        T, d = x.shape
-        xb = _as_bf16(x).contiguous()
-        gwb, gbb = _as_bf16(gate_w).contiguous(), _as_bf16(gate_b).contiguous()
-        wb = [_as_bf16(w).contiguous() for w in weights]
-        G = E + (1 if has_shared else 0)
-        w1s, w3s, w2s = wb[0::3][:G], wb[1::3][:G], wb[2::3][:G]
-
-        idx, idx64, w, v = K.router_fwd(xb, gwb, gbb, k, rs)
-        counts, offsets, perm, pos, x_perm = K.dispatch(idx, xb, E)
-        rows_r, rows_s = T * k, (T if has_shared else 0)
-        ab, h = K.gateup_fwd(x_perm, xb if has_shared else None, offsets, E, w1s, w3s, inter)
-        o = K.down_fwd(h, offsets, E, rows_r, rows_s, w2s, d)
-        y = K.combine_fwd(o, idx, w, pos, rows_r, has_shared, out_dtype)
+        fw = _forward_pass(meta, x, gate_w, gate_b, weights)
+        xb, gwb, wb, idx, idx64, w, v, counts, offsets, perm, pos, x_perm, ab, h, o, y = fw
 
         # Experts that get no tokens return None gradients (the reference never
         # puts them in the graph, moe.py:66-72).  Their counts travel to the
@@ -167,14 +178,21 @@ class DeepSeekMoE(nn.Module):
         self._last_weights: torch.Tensor | None = None
 
     def _flat_weights(self) -> list[torch.Tensor]:
+        # Direct dict access: nn.Module.__getattr__ per weight dominates the
+        # host time of a decode-sized call otherwise.
         ws = []
-        mods = list(self.experts) + ([self.shared_expert] if self.shared_expert is not None else [])
+        mods = list(self.experts._modules.values())
+        if self.shared_expert is not None:
+            mods.append(self.shared_expert)
         for m in mods:
-            ws += [m.w1.weight, m.w3.weight, m.w2.weight]
+            sub = m._modules
+            ws += [sub["w1"]._parameters["weight"], sub["w3"]._parameters["weight"],
+                   sub["w2"]._parameters["weight"]]
         return ws
 
-    def _output_dtype(self, x: torch.Tensor) -> torch.dtype:
-        params_bf16 = all(p.dtype == torch.bfloat16 for p in self.parameters())
+    def _output_dtype(self, x: torch.Tensor, weights: list[torch.Tensor]) -> torch.dtype:
+        params_bf16 = (self.gate.weight.dtype == torch.bfloat16 and self.gate.bias.dtype == torch.bfloat16
+                       and all(w.dtype == torch.bfloat16 for w in weights))
         if torch.is_autocast_enabled("cuda"):
             if torch.get_autocast_dtype("cuda") != torch.bfloat16:
                 raise NotImplementedError("fusionllm_amd.DeepSeekMoE supports bf16 autocast only")
@@ -192,14 +210,24 @@ class DeepSeekMoE(nn.Module):
         flat = x.view(-1, self.dim)
         if not flat.is_cuda:
             raise RuntimeError("fusionllm_amd.DeepSeekMoE runs on a ROCm device only (got a CPU tensor)")
-        out_dtype = self._output_dtype(flat)
+        weights = self._flat_weights()
+        out_dtype = self._output_dtype(flat, weights)
         E, k = self.n_routed_experts, self.n_activated_experts
         if flat.shape[0] == 0:
             return self._forward_empty(flat, out_dtype).view(shape)
         meta = (E, k, self.moe_inter_dim, float(self.route_scale), self.shared_expert is not None, out_dtype)
-        with torch.cuda.device(flat.device):
-            y, idx64, w = _MoEBlockFunction.apply(meta, flat, self.gate.weight, self.gate.bias,
-                                                  *self._flat_weights())
+        needs_grad = torch.is_grad_enabled() and (
+            flat.requires_grad or self.gate.weight.requires_grad or self.gate.bias.requires_grad
+            or any(t.requires_grad for t in weights))
+        # Switch devices only when needed (the context manager costs host time).
+        switch = flat.device.index != torch._C._cuda_getDevice()
+        with torch.cuda.device(flat.device) if switch else contextlib.nullcontext():
+            if needs_grad:
+                y, idx64, w = _MoEBlockFunction.apply(meta, flat, self.gate.weight, self.gate.bias, *weights)
+            else:
+                # inference: the same kernels, nothing kept for a backward pass
+                fw = _forward_pass(meta, flat, self.gate.weight, self.gate.bias, weights)
+                idx64, w, y = fw[4], fw[5], fw[-1]
         self._last_indices = idx64
         self._last_weights = w
         return y.view(shape)
