@@ -19,7 +19,10 @@
 // MFMA blocks; fragment layout of v_mfma_f32_32x32x16_bf16: lane l supplies
 // A[l%32][8*(l/32) .. +7] and B[8*(l/32) .. +7][l%32] and receives
 // C[8*(r/4) + 4*(l/32) + r%4][l%32] in accumulator r.
+#include <atomic>
+
 #include "fmoe_common.h"
+#include "gemm_core.h"
 
 namespace fmoe {
 
@@ -173,184 +176,286 @@ struct GemmArgs {
   int small_max;  // groups with 1 .. small_max rows go to small_gemm_kernel (0: none)
 };
 
-// Epilogue staging: the tile's bf16 values in LDS, row-major with 512 bytes
-// per row; 16-byte chunk c of row r sits at chunk position c ^ (r & 31), so
-// both the MFMA-layout 2-byte writes and the row-chunk 16-byte reads are free
-// of bank conflicts.
-__device__ __forceinline__ uint32_t stage_off(int row, int col) {
-  return static_cast<uint32_t>(row) * 512u +
-         (static_cast<uint32_t>((col >> 3) ^ (row & 31)) << 4) + static_cast<uint32_t>(col & 7) * 2u;
+// ---- tiled row-grouped kernel ----------------------------------------------
+// Persistent: a grid of at most one workgroup per CU walks the tiles
+// t = blockIdx.x, blockIdx.x + gridDim.x, ...  Tiles are enumerated group by
+// group (experts 0..E-1, then the shared expert), m tile major; the tile ->
+// (group, rows) map comes from offsets[] on the device.  The global -> LDS
+// copies run as one continuous two-stage ring over all K steps of all of a
+// workgroup's tiles, so the next tile's first operands arrive while the current
+// tile finishes and writes its epilogue.  Rows past a group's end and weight
+// rows past N are clamped to the last valid one (their products are never
+// stored), so no operand is read out of bounds.
+
+// Tile t -> (group g, m tile tm, n tile tn, first row, group rows); false if t
+// is past the last tile.
+// offsets: args.offsets passed as a separate restrict pointer, so that these
+// uniform reads become scalar loads (a vector load would need a vmcnt wait that
+// also waits for the in-flight operand copies).
+__device__ __forceinline__ bool locate_tile(const GemmArgs& a, const int32_t* __restrict__ offsets, int tiles_n,
+                                            int t, int& g, int& tm, int& tn, int& row_base, int& M) {
+  const int G = a.E + (a.rows_shared > 0 ? 1 : 0);
+  for (g = 0; g < G; ++g) {
+    if (g < a.E) {
+      const int2 o = core::sload2(offsets + g);
+      row_base = o.x;
+      M = o.y - o.x;
+    } else {
+      row_base = a.rows_routed;
+      M = a.rows_shared;
+    }
+    const int nt = (M <= a.small_max) ? 0 : ((M + core::BM - 1) / core::BM) * tiles_n;
+    if (t < nt) {
+      tm = t / tiles_n;
+      tn = t - tm * tiles_n;
+      return true;
+    }
+    t -= nt;
+  }
+  return false;
 }
 
-template <class C, int MODE>
-__global__ __launch_bounds__(C::NT) void grouped_gemm_kernel(const GemmArgs args) {
-  static_assert(C::BM == 256 && C::BN == 256, "epilogue staging assumes a 256 x 256 tile");
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::STAGE_BYTES];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+__device__ __forceinline__ int count_tiles(const GemmArgs& a, const int32_t* __restrict__ offsets, int tiles_n) {
+  const int G = a.E + (a.rows_shared > 0 ? 1 : 0);
+  int total = 0;
+  for (int g = 0; g < G; ++g) {
+    int M = a.rows_shared;
+    if (g < a.E) {
+      const int2 o = core::sload2(offsets + g);
+      M = o.y - o.x;
+    }
+    total += (M <= a.small_max) ? 0 : ((M + core::BM - 1) / core::BM) * tiles_n;
+  }
+  return total;
+}
 
-  // Columns covered by one tile: GATEUP_FWD interleaves w1 and w3 rows, so a
-  // tile of BN accumulator columns covers BN/2 columns of h.
-  constexpr int TN_COLS = (MODE == GATEUP_FWD) ? C::BN / 2 : C::BN;
+// Store instructions per lane in the epilogue of a full tile (they may still
+// be in flight at the next barrier; see the wait there).
+template <int MODE>
+constexpr int epi_stores() {
+  return MODE == GATEUP_FWD ? 24 : (MODE == DOWN_BWD ? 32 : 16);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs args,
+                                                                 const int32_t* __restrict__ offsets) {
+  using namespace core;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w / WN, wn = w % WN;
+  const uint32_t sbase = lds_addr(smem);
+
+  // GATEUP_FWD: a tile covers 128 h columns (128 rows of w1 and of w3).
+  constexpr int TN_COLS = (MODE == GATEUP_FWD) ? BN / 2 : BN;
   const int tiles_n = (args.N + TN_COLS - 1) / TN_COLS;
+  const int total_tiles = count_tiles(args, offsets, tiles_n);
+  const int my_tiles = (total_tiles - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) /
+                       static_cast<int>(gridDim.x);
+  if (my_tiles <= 0) return;
+  const int nk = args.K / BK;
+  const int total = my_tiles * nk;  // K steps of 64 over all of this workgroup's tiles
 
-  // ---- tile -> (group, m tile, n tile)
-  const int G = args.E + (args.rows_shared > 0 ? 1 : 0);
-  int tile = blockIdx.x;
-  int g = 0, M = 0, row_base = 0;
-  for (; g < G; ++g) {
-    if (g < args.E) {
-      row_base = args.offsets[g];
-      M = args.offsets[g + 1] - row_base;
-    } else {
-      row_base = args.rows_routed;
-      M = args.rows_shared;
-    }
-    const int nt = (M <= args.small_max) ? 0 : ((M + C::BM - 1) / C::BM) * tiles_n;
-    if (tile < nt) break;
-    tile -= nt;
-  }
-  if (g >= G) return;  // grid is an upper bound on the tile count
-  const int tm = tile / tiles_n, tn = tile % tiles_n;
-  const int m0 = tm * C::BM;
-  const int n0 = tn * TN_COLS;
-
-  const uint16_t* A = (g < args.E || args.a_shared == nullptr)
-                          ? args.a_routed + static_cast<int64_t>(row_base) * args.lda
-                          : args.a_shared;
-
-  // ---- operand loaders (both K-contiguous)
-  KLoad<C::BM, C::NT> la;
+  // ---- global -> LDS copy cursor
+  // Copy instruction i of wave w writes LDS rows 64 i + 8 w .. +7 of an operand;
+  // lane l fetches row 64 i + drow, global chunk dchunk (the swizzled slot l % 8).
+  const int drow = w * 8 + (lane >> 3);
+  const int dchunk = (lane & 7) ^ swz(drow);  // swz(64 i + drow) == swz(drow)
+  const uint32_t lds_copy = sbase + w * 1024;
+  int c_ti = 0, c_kt = 0;
+  const uint16_t* c_a = nullptr;   // A rows of the tile being copied
+  const uint16_t* c_b0 = nullptr;  // B operand base(s)
+  const uint16_t* c_b1 = nullptr;
+  int c_last_row = 0, c_n0 = 0;    // last valid A row of the tile, first B row
+  auto copy_tile = [&](int ti) {
+    int g, tm, tn, row_base, M;
+    locate_tile(args, offsets, tiles_n, static_cast<int>(blockIdx.x) + ti * static_cast<int>(gridDim.x), g, tm, tn, row_base,
+                M);
+    const uint16_t* A = (g < args.E || args.a_shared == nullptr) ? args.a_routed + static_cast<int64_t>(row_base) * args.lda
+                                                                 : args.a_shared;
+    c_a = A + static_cast<int64_t>(tm) * BM * args.lda;
+    c_last_row = min(M - tm * BM, BM) - 1;
+    c_b0 = args.b0[g];
+    c_b1 = args.b1[g];
+    c_n0 = tn * TN_COLS;
+  };
+  copy_tile(0);
+  const int lda = static_cast<int>(args.lda), ldb = static_cast<int>(args.ldb);
+  auto issue = [&](int it) {
+    const uint32_t st = lds_copy + (it & 1) * STAGE;
+    const int kofs = c_kt * BK;
 #pragma unroll
-  for (int i = 0; i < la.PER; ++i) {
-    int r = m0 + KLoad<C::BM, C::NT>::row_of(tid, i);
-    r = r < M ? r : M - 1;
-    la.src[i] = A + static_cast<int64_t>(r) * args.lda + KLoad<C::BM, C::NT>::chunk_of(tid) * 8;
-  }
-  KLoad<C::BN, C::NT> lb;
-  const uint16_t* W0 = args.b0[g];
-  const uint16_t* W1 = args.b1[g];
-#pragma unroll
-  for (int i = 0; i < lb.PER; ++i) {
-    const int r = KLoad<C::BN, C::NT>::row_of(tid, i);
-    const uint16_t* base = W0;
-    int n;
-    if constexpr (MODE == GATEUP_FWD) {
-      // accumulator column block fn of wave column wb: even fn -> w1, odd -> w3,
-      // both for h columns n0 + wb*WTN/2 + (fn/2)*32 + i.
-      const int wb = r / C::WTN, within = r % C::WTN, fn = within / 32;
-      n = n0 + wb * (C::WTN / 2) + (fn / 2) * 32 + (within % 32);
-      base = (fn & 1) ? W1 : W0;
-    } else {
-      n = n0 + r;
+    for (int i = 0; i < LA; ++i) {
+      const int r = min(64 * i + drow, c_last_row);
+      copy16(st + i * 8192, c_a + kofs, static_cast<uint32_t>(r * lda + dchunk * 8) * 2u);
     }
-    n = n < args.N ? n : args.N - 1;
-    lb.src[i] = base + static_cast<int64_t>(n) * args.ldb + KLoad<C::BN, C::NT>::chunk_of(tid) * 8;
-  }
-
-  auto store_tile = [&](int buf) {
-    uint8_t* sA = smem + buf * C::STAGE_BYTES;
-    la.store(sA, tid);
-    lb.store(sA + C::A_BYTES, tid);
+#pragma unroll
+    for (int i = 0; i < LB; ++i) {
+      // GATEUP_FWD bands: w1 rows (even i) and w3 rows (odd i), 64 h columns each
+      const int n = min(c_n0 + ((MODE == GATEUP_FWD) ? (i >> 1) * 64 : 64 * i) + drow, args.N - 1);
+      const uint16_t* b = (MODE == GATEUP_FWD && (i & 1)) ? c_b1 : c_b0;
+      copy16(st + A_BYTES + i * 8192, b + kofs, static_cast<uint32_t>(n * ldb + dchunk * 8) * 2u);
+    }
+    if (++c_kt == nk) {
+      c_kt = 0;
+      if (++c_ti < my_tiles) copy_tile(c_ti);
+    }
   };
 
-  f32x16 acc[C::FM][C::FN];
-#pragma unroll
-  for (int fm = 0; fm < C::FM; ++fm)
-#pragma unroll
-    for (int fn = 0; fn < C::FN; ++fn)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
+  // ---- fragment address bases (A rows / B rows of this wave)
+  uint32_t xa = frag_base(wm * WTM, lane);
+  uint32_t xb = frag_base(wn * WTN, lane);
 
-  const int nk = args.K / kBK;
-  la.load(0);
-  lb.load(0);
-  store_tile(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) {
-      la.load((kt + 1) * kBK);
-      lb.load((kt + 1) * kBK);
-    }
-    const uint8_t* sA = smem + buf * C::STAGE_BYTES;
-    mma_ktile<C>(sA, sA + C::A_BYTES, acc, wm, wn, lane);
-    if (kt + 1 < nk) store_tile(buf ^ 1);
-    __syncthreads();
-  }
-
-  // ---- epilogue, phase 1: bf16-rounded accumulators into the LDS stage
-  // (the loop ended with a barrier, so both operand stages are free).
-  // GATEUP_FWD stages a in columns 0..127 and b in 128..255 (h column order).
-  uint8_t* cs = smem;
-  const int row_l = (lane >> 5) * 4;
-#pragma unroll
-  for (int fm = 0; fm < C::FM; ++fm) {
-#pragma unroll
-    for (int fn = 0; fn < C::FN; ++fn) {
-      int col;
-      if constexpr (MODE == GATEUP_FWD)
-        col = (fn & 1) * 128 + wn * (C::WTN / 2) + (fn / 2) * 32 + (lane & 31);
-      else
-        col = wn * C::WTN + fn * 32 + (lane & 31);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = wm * C::WTM + fm * 32 + (r >> 2) * 8 + row_l + (r & 3);
-        *reinterpret_cast<uint16_t*>(cs + stage_off(row, col)) = f2bf(acc[fm][fn][r]);
-      }
-    }
-  }
-  __syncthreads();
-
-  // ---- epilogue, phase 2: 16-byte chunks of whole rows
-  if constexpr (MODE == GATEUP_FWD) {
-    // 256 rows x 16 chunks of h; a chunk c pairs a (staged chunk c) and b (16 + c)
-    for (int idx = tid; idx < C::BM * 16; idx += C::NT) {
-      const int row = idx >> 4, c = idx & 15;
-      const int col = n0 + c * 8;
-      if (m0 + row >= M || col >= args.N) continue;
-      const uint4 av = *reinterpret_cast<const uint4*>(cs + stage_off(row, c * 8));
-      const uint4 bv = *reinterpret_cast<const uint4*>(cs + stage_off(row, 128 + c * 8));
-      float af[8], bfv[8], hf[8];
-      unpack8(av, af);
-      unpack8(bv, bfv);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) hf[i] = bf_round(af[i] * fast_sigmoid(af[i])) * bfv[i];
-      const int64_t grow = row_base + m0 + row;
-      *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + col) = av;
-      *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + args.inter + col) = bv;
-      *reinterpret_cast<uint4*>(args.c1 + grow * args.ldc1 + col) = pack8(hf);
-    }
+  issue(0);
+  if (total > 1) {
+    issue(1);
+    wait_vm_barrier<LT>();
   } else {
-    for (int idx = tid; idx < C::BM * 32; idx += C::NT) {
-      const int row = idx >> 5, c = idx & 31;
-      const int col = n0 + c * 8;
-      if (m0 + row >= M || col >= args.N) continue;
-      const uint4 v = *reinterpret_cast<const uint4*>(cs + stage_off(row, c * 8));
-      const int64_t grow = row_base + m0 + row;
-      if constexpr (MODE == DOWN_BWD) {
-        // h = s * b with s = bf16(silu(a)); dh arrives bf16-rounded:
-        // da = bf16(bf16(dh * b) * silu'(a)), db = bf16(dh * s)
-        const uint4 avv = *reinterpret_cast<const uint4*>(args.aux + grow * args.ldaux + col);
-        const uint4 bvv = *reinterpret_cast<const uint4*>(args.aux + grow * args.ldaux + args.inter + col);
-        float dh[8], af[8], bfv[8], da[8], db[8];
-        unpack8(v, dh);
-        unpack8(avv, af);
-        unpack8(bvv, bfv);
+    wait_vm_barrier<0>();
+  }
+  bf16x8 P[FN], Q[2][4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float sg = fast_sigmoid(af[i]);
-          const float sv = bf_round(af[i] * sg);
-          const float ds = bf_round(dh[i] * bfv[i]);
-          da[i] = ds * (sg * (1.0f + af[i] * (1.0f - sg)));
-          db[i] = dh[i] * sv;
+  for (int p = 0; p < FN; ++p)
+    P[p] = *reinterpret_cast<const bf16x8*>(smem + A_BYTES + ((xb ^ ((p & 3) << 5)) + 2048u * p));
+#pragma unroll
+  for (int q = 0; q < 4; ++q) Q[0][q] = *reinterpret_cast<const bf16x8*>(smem + ((xa ^ ((q & 3) << 5)) + 2048u * q));
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  uint8_t* ep = smem + 2 * STAGE + w * EPI;  // this wave's epilogue staging (4 KB)
+  int e_ti = 0, e_kt = 0;
+  int last_epi = -4;        // iteration whose end wrote an epilogue
+  bool last_full = false;   // that epilogue issued exactly epi_stores<MODE>() stores
+  for (int it = 0; it < total; ++it) {
+    // keep the per-step fragment addresses from being hoisted out of the loop
+    asm volatile("" : "+v"(xa), "+v"(xb));
+    const uint32_t cur = sbase + (it & 1) * STAGE;
+    kstep<64>(acc, P, Q[0], Q[1], xa, xb, cur);  // reads the second K half of this stage
+    uint32_t src = cur;                           // the last step re-reads (harmlessly) its own stage
+    if (it + 1 < total) {
+      // Stage (it+1) must have landed; stage it&1 is free once every wave is past
+      // this point.  Stores of an epilogue written after copy it+1 was issued may
+      // still be in flight (only when their number is exact).
+      if (it - last_epi == 1 && last_full)
+        wait_vm_barrier<epi_stores<MODE>()>();
+      else
+        wait_vm_barrier<0>();
+      if (it + 2 < total) issue(it + 2);
+      src = sbase + ((it + 1) & 1) * STAGE;
+    }
+    kstep<0>(acc, P, Q[1], Q[0], xa, xb, src);
+
+    if (++e_kt < nk) continue;
+    // ---- tile epilogue: this wave's 64 x 128 block
+    e_kt = 0;
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3\n" ::: "memory");  // MFMA results -> VALU reads
+    int g, tm, tn, row_base, M;
+    locate_tile(args, offsets, tiles_n, static_cast<int>(blockIdx.x) + e_ti * static_cast<int>(gridDim.x), g, tm, tn,
+                row_base, M);
+    const int rows_valid = min(M - tm * BM, BM);
+    const int col0 = tn * TN_COLS + wn * (TN_COLS / WN);  // first output column of this wave
+    const bool full = rows_valid == BM && (tn + 1) * TN_COLS <= args.N;
+    const int64_t grow0 = static_cast<int64_t>(row_base) + tm * BM + wm * WTM;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      // stage rows 16 i .. 16 i + 15 of the wave block, 128 accumulator columns
+      // (256 bytes per row; chunk c of row r at slot c ^ r)
+      {
+        const int r = lane & 15;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int col = j * 16 + (lane >> 4) * 4;
+          const uint32_t off = r * 256 + ((((col >> 3) ^ r)) << 4) + (col & 7) * 2;
+          uint2 v;
+          v.x = pack2(acc[i][j][0], acc[i][j][1]);
+          v.y = pack2(acc[i][j][2], acc[i][j][3]);
+          *reinterpret_cast<uint2*>(ep + off) = v;
         }
-        *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + col) = pack8(da);
-        *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + args.inter + col) = pack8(db);
-      } else {
-        *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + col) = v;
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int r = t * 4 + (lane >> 4), c = lane & 15;
+        const uint4 v = *reinterpret_cast<const uint4*>(ep + r * 256 + ((c ^ r) << 4));
+        const int lrow = wm * WTM + i * 16 + r;
+        const int64_t grow = grow0 + i * 16 + r;
+        if constexpr (MODE == GATEUP_FWD) {
+          // columns 0..63: a, 64..127: b for h columns col0 .. col0 + 63
+          const int hc = col0 + (c & 7) * 8;
+          if (full || (lrow < rows_valid && hc < args.N)) {
+            uint16_t* dst = args.c0 + grow * args.ldc0 + (c < 8 ? 0 : args.inter) + hc;
+            *reinterpret_cast<uint4*>(dst) = v;
+          }
+        } else if constexpr (MODE == DOWN_BWD) {
+          // h = s * b, s = bf16(silu(a)); dh arrives bf16-rounded:
+          // da = bf16(bf16(dh * b) * silu'(a)), db = bf16(dh * s)
+          const int hc = col0 + c * 8;
+          if (full || (lrow < rows_valid && hc < args.N)) {
+            const uint4 avv = *reinterpret_cast<const uint4*>(args.aux + grow * args.ldaux + hc);
+            const uint4 bvv = *reinterpret_cast<const uint4*>(args.aux + grow * args.ldaux + args.inter + hc);
+            float dh[8], af[8], bfv[8], da[8], db[8];
+            unpack8(v, dh);
+            unpack8(avv, af);
+            unpack8(bvv, bfv);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float sg = fast_sigmoid(af[e]);
+              const float sv = bf_round(af[e] * sg);
+              const float ds = bf_round(dh[e] * bfv[e]);
+              da[e] = ds * (sg * (1.0f + af[e] * (1.0f - sg)));
+              db[e] = dh[e] * sv;
+            }
+            *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + hc) = pack8(da);
+            *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + args.inter + hc) = pack8(db);
+          }
+        } else {
+          const int oc = col0 + c * 8;
+          if (full || (lrow < rows_valid && oc < args.N))
+            *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + oc) = v;
+        }
+      }
+      if constexpr (MODE == GATEUP_FWD) {
+        // h = bf16(bf16(silu(a)) * b) for the 16 rows x 64 h columns, staged as
+        // 128-byte rows (chunk c of row r at slot c ^ swz(r))
+        const int r = lane & 15;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float hv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float a = bf_round(acc[i][j][e]);
+            const float b = bf_round(acc[i][j + 4][e]);
+            hv[e] = bf_round(a * fast_sigmoid(a)) * b;
+          }
+          const int col = j * 16 + (lane >> 4) * 4;
+          const uint32_t off = r * 128 + ((((col >> 3) ^ swz(r))) << 4) + (col & 7) * 2;
+          uint2 v;
+          v.x = pack2(hv[0], hv[1]);
+          v.y = pack2(hv[2], hv[3]);
+          *reinterpret_cast<uint2*>(ep + off) = v;
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int rr = t * 8 + (lane >> 3), c = lane & 7;
+          const uint4 v = *reinterpret_cast<const uint4*>(ep + rr * 128 + ((c ^ swz(rr)) << 4));
+          const int lrow = wm * WTM + i * 16 + rr;
+          const int hc = col0 + c * 8;
+          if (full || (lrow < rows_valid && hc < args.N))
+            *reinterpret_cast<uint4*>(args.c1 + (grow0 + i * 16 + rr) * args.ldc1 + hc) = v;
+        }
       }
     }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    asm volatile("s_nop 1" ::: "memory");  // VALU writes -> MFMA reads of the accumulators
+    last_epi = it;
+    last_full = full;
+    ++e_ti;
   }
 }
 
@@ -631,7 +736,6 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const WgradArgs args)
 }
 
 // ---- host side --------------------------------------------------------------
-using CfgRow = Cfg<256, 256, 2, 4>;    // 512 threads, wave tile 128 x 64
 using CfgWgrad = Cfg<256, 256, 2, 4>;
 
 int check_common(int n_experts, int64_t rows_routed, int64_t rows_shared, int64_t dim, int64_t inter) {
@@ -647,17 +751,30 @@ int check_common(int n_experts, int64_t rows_routed, int64_t rows_shared, int64_
 // kernel for every group.
 constexpr int64_t kSmallLaunchRows = 4096;
 
-template <class C, int MODE>
+// Compute units of the current device (the persistent grid size), cached per
+// device ordinal.
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+  cache[dev].store(v, std::memory_order_relaxed);
+  return v;
+}
+
+template <int MODE>
 int launch_rows(GemmArgs& a, int64_t rows_routed, int64_t rows_shared, int E, void* stream) {
-  constexpr int TN_COLS = (MODE == GATEUP_FWD) ? C::BN / 2 : C::BN;
+  constexpr int TN_COLS = (MODE == GATEUP_FWD) ? core::BN / 2 : core::BN;
   const int64_t tiles_n = ceil_div(a.N, TN_COLS);
   constexpr bool kHasSmall = (MODE == GATEUP_FWD || MODE == DOWN_FWD);
   a.small_max = (kHasSmall && rows_routed + rows_shared <= kSmallLaunchRows) ? kSmallM : 0;
   // Upper bound of sum over groups of ceil(M_g / BM): floor(rows/BM) + groups.
-  const int64_t mt = rows_routed / C::BM + E + ceil_div(rows_shared, C::BM);
-  const int64_t grid = mt * tiles_n;
-  if (grid <= 0) return FMOE_OK;
-  grouped_gemm_kernel<C, MODE><<<dim3(grid), dim3(C::NT), 0, as_stream(stream)>>>(a);
+  const int64_t tiles = (rows_routed / core::BM + E + ceil_div(rows_shared, core::BM)) * tiles_n;
+  if (tiles <= 0) return FMOE_OK;
+  const int64_t grid = tiles < device_cus() ? tiles : device_cus();
+  rows_gemm_kernel<MODE><<<dim3(grid), dim3(core::NT), 0, as_stream(stream)>>>(a, a.offsets);
   if constexpr (kHasSmall) {
     if (a.small_max > 0) {
       const int G = E + (rows_shared > 0 ? 1 : 0);
@@ -709,7 +826,7 @@ extern "C" int fmoe_gateup_fwd(const void* x_routed, const void* x_shared, const
     a.b0[g] = static_cast<const uint16_t*>(w1[g]);
     a.b1[g] = static_cast<const uint16_t*>(w3[g]);
   }
-  return launch_rows<CfgRow, GATEUP_FWD>(a, rows_routed, rows_shared, n_experts, stream);
+  return launch_rows<GATEUP_FWD>(a, rows_routed, rows_shared, n_experts, stream);
 }
 
 extern "C" int fmoe_down_fwd(const void* h, const int32_t* offsets, int n_experts,
@@ -736,7 +853,7 @@ extern "C" int fmoe_down_fwd(const void* h, const int32_t* offsets, int n_expert
     if (!w2[g]) return FMOE_ERR_INVALID_ARG;
     a.b0[g] = static_cast<const uint16_t*>(w2[g]);
   }
-  return launch_rows<CfgRow, DOWN_FWD>(a, rows_routed, rows_shared, n_experts, stream);
+  return launch_rows<DOWN_FWD>(a, rows_routed, rows_shared, n_experts, stream);
 }
 
 extern "C" int fmoe_down_bwd_dx(const void* d_out_routed, const void* d_out_shared,
@@ -765,7 +882,7 @@ extern "C" int fmoe_down_bwd_dx(const void* d_out_routed, const void* d_out_shar
   a.ldaux = 2 * inter;
   const int G = n_experts + (rows_shared > 0 ? 1 : 0);
   for (int g = 0; g < G; ++g) a.b0[g] = static_cast<const uint16_t*>(w2t) + static_cast<int64_t>(g) * inter * dim;
-  return launch_rows<CfgRow, DOWN_BWD>(a, rows_routed, rows_shared, n_experts, stream);
+  return launch_rows<DOWN_BWD>(a, rows_routed, rows_shared, n_experts, stream);
 }
 
 extern "C" int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int n_experts,
@@ -790,7 +907,7 @@ extern "C" int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int 
   const int G = n_experts + (rows_shared > 0 ? 1 : 0);
   for (int g = 0; g < G; ++g)
     a.b0[g] = static_cast<const uint16_t*>(w13t) + static_cast<int64_t>(g) * dim * 2 * inter;
-  return launch_rows<CfgRow, GATEUP_BWD>(a, rows_routed, rows_shared, n_experts, stream);
+  return launch_rows<GATEUP_BWD>(a, rows_routed, rows_shared, n_experts, stream);
 }
 
 namespace fmoe {
