@@ -705,6 +705,196 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(const WgradArgs args) {
   }
 }
 
+// ---- weight gradients on the shared core ------------------------------------
+// Both operands are MN-contiguous ([rows, m_out] and [rows, n_out]), so their
+// 64 x 256 stage tiles are copied as they lie in memory (K-major: 64 k rows of
+// 512 bytes) with the same global -> LDS copies as the row products, and the
+// MFMA fragments are read with ds_read_b64_tr_b16, which returns to lane
+// (h = l / 16, i = l % 16) of each 16-lane group the i-th column of the 4 x 4
+// block of 16-bit values that source lanes 4 j + q address (row j, 4 values at
+// column 4 q): two such reads give a lane 8 consecutive k of one output row.
+// The 32-byte windows of a k row are XOR-swizzled by wsw(row) so that the 16
+// rows x 32 bytes a read instruction touches fall on distinct banks.
+__device__ __forceinline__ int wsw(int r) { return (r & 3) | (((r >> 3) & 1) << 2); }
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x8 tr_frag(uint32_t addr) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)addr);
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)(addr + 2048u));
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+__global__ __launch_bounds__(core::NT, 1) void wgrad_tr_kernel(const WgradArgs args,
+                                                               const int32_t* __restrict__ offsets) {
+  using namespace core;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w / WN, wn = w % WN;  // wave block: 64 m x 128 n
+  const uint32_t sbase = lds_addr(smem);
+  const int tiles_m = (args.m_out + BM - 1) / BM, tiles_n = (args.n_out + BN - 1) / BN;
+  const int tiles = tiles_m * tiles_n;
+  const int G = args.E + (args.rows_shared > 0 ? 1 : 0);
+
+  // ---- work unit -> (group, K chunk, output tile)
+  int unit = blockIdx.x;
+  int g = 0, row_base = 0, M = 0, chunks = 0, pbase = 0;
+  for (; g < G; ++g) {
+    if (g < args.E) {
+      const int2 o = core::sload2(offsets + g);
+      row_base = o.x;
+      M = o.y - o.x;
+    } else {
+      row_base = args.rows_routed;
+      M = args.rows_shared;
+    }
+    chunks = (M + args.kc - 1) / args.kc;
+    const int nu = chunks * tiles;
+    if (unit < nu) break;
+    unit -= nu;
+    if (chunks > 1) pbase += chunks;
+  }
+  if (g >= G) return;
+  const int chunk = unit / tiles, tile = unit - chunk * tiles;
+  const int tm = tile / tiles_n, tn = tile - tm * tiles_n;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int k_begin = chunk * args.kc;
+  const int k_end = min(M, k_begin + args.kc);
+  const int nk = (k_end - k_begin + BK - 1) / BK;
+  const bool shared_sep = (g >= args.E);
+  const uint16_t* A = (shared_sep && args.a_shared) ? args.a_shared : args.a_routed + static_cast<int64_t>(row_base) * args.lda;
+  const uint16_t* B = (shared_sep && args.b_shared) ? args.b_shared : args.b_routed + static_cast<int64_t>(row_base) * args.ldb;
+  const int lda = static_cast<int>(args.lda), ldb = static_cast<int>(args.ldb);
+
+  // ---- copies: instruction i of wave w writes k rows 16 i + drow (1 KB = 2 rows of 512 B);
+  // lane chunk p = l % 32 holds logical chunk c of the row
+  const int drow = 2 * w + (lane >> 5);
+  const int p = lane & 31;
+  const int c = (((p >> 1) ^ wsw(drow)) << 1) | (p & 1);  // wsw(16 i + drow) == wsw(drow)
+  const int colA = min(m0 + 8 * c, args.m_out - 8), colB = min(n0 + 8 * c, args.n_out - 8);
+  const uint32_t lds_copy = sbase + w * 1024;
+  auto issue = [&](int kt) {
+    const int k0 = k_begin + kt * BK;
+    const int last = k_end - 1 - k0;  // last valid k row of this stage
+    const uint32_t st = lds_copy + (kt & 1) * STAGE;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = min(16 * i + drow, last);
+      copy16(st + i * 8192, A + static_cast<int64_t>(k0) * lda, static_cast<uint32_t>(r * lda + colA) * 2u);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = min(16 * i + drow, last);
+      copy16(st + A_BYTES + i * 8192, B + static_cast<int64_t>(k0) * ldb, static_cast<uint32_t>(r * ldb + colB) * 2u);
+    }
+  };
+  // Rows past k_end in a stage hold copies of the last valid row: zero their A
+  // side (after this wave's copies have landed) so that they add nothing.
+  auto zero_tail = [&](int kt) {
+    const int k0 = k_begin + kt * BK;
+    if (k_end - k0 >= BK) return;
+    uint8_t* st = smem + (kt & 1) * STAGE + w * 1024 + lane * 16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (k0 + 16 * i + drow >= k_end) *reinterpret_cast<uint4*>(st + i * 8192) = make_uint4(0, 0, 0, 0);
+  };
+  auto sync_stage = [&](int kt, bool more_in_flight) {
+    if (more_in_flight) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    zero_tail(kt);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+
+  // ---- fragment addresses: lane (h, s = 4 jq + q); window swizzle fr = wsw(8 h + jq)
+  const int h = lane >> 4, jq = (lane >> 2) & 3, q = lane & 3;
+  const int fr = jq | ((h & 1) << 2);
+  const uint32_t xa = static_cast<uint32_t>((8 * h + jq) * 512 + (((4 * wm) ^ fr) << 5) + 8 * q);
+  const uint32_t xb = static_cast<uint32_t>(A_BYTES + (8 * h + jq) * 512 + ((8 * wn + fr) << 5) + 8 * q);
+
+  issue(0);
+  if (nk > 1) issue(1);
+  sync_stage(0, nk > 1);
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  bf16x8 fa[FM], fb[FN];
+#pragma unroll
+  for (int f = 0; f < FM; ++f) fa[f] = tr_frag(sbase + (xa ^ (f << 5)));
+#pragma unroll
+  for (int f = 0; f < FN; ++f) fb[f] = tr_frag(sbase + (xb ^ (f << 5)));
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const uint32_t cur = sbase + (kt & 1) * STAGE;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      uint32_t src = cur + 16384u;  // second K half of this stage
+      if (ks == 1) {
+        src = cur;  // the last step re-reads (harmlessly) its own stage
+        if (kt + 1 < nk) {
+          sync_stage(kt + 1, false);
+          if (kt + 2 < nk) issue(kt + 2);
+          src = sbase + ((kt + 1) & 1) * STAGE;
+        }
+      }
+      bf16x8 na[FM], nb[FN];
+#pragma unroll
+      for (int f = 0; f < FM; ++f) na[f] = tr_frag(src + (xa ^ (f << 5)));
+#pragma unroll
+      for (int f = 0; f < FN; ++f) nb[f] = tr_frag(src + (xb ^ (f << 5)));
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+      // interleave: per 8 MFMAs, 6 fragment reads (24 reads, 32 MFMAs per step)
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+#pragma unroll
+      for (int f = 0; f < FM; ++f) fa[f] = na[f];
+#pragma unroll
+      for (int f = 0; f < FN; ++f) fb[f] = nb[f];
+    }
+  }
+
+  // ---- epilogue: lane holds C[m0 + 64 wm + 16 i + l % 16][n0 + 128 wn + 16 j + 4 (l / 16) + 0..3]
+  const int64_t mn = static_cast<int64_t>(args.m_out) * args.n_out;
+  float* part = (chunks > 1) ? args.partial + static_cast<int64_t>(pbase + chunk) * mn : nullptr;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int m = m0 + wm * WTM + i * 16 + (lane & 15);
+    if (m >= args.m_out) continue;
+    const bool lo = m < args.m_split;
+    void* base = lo ? args.out_lo[g] : args.out_hi[g];
+    const int64_t orow = static_cast<int64_t>(lo ? m : m - args.m_split) * args.n_out;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + wn * WTN + j * 16 + (lane >> 4) * 4;
+      if (n >= args.n_out) continue;
+      const f32x4 v = acc[i][j];
+      if (part) {
+        *reinterpret_cast<f32x4*>(part + static_cast<int64_t>(m) * args.n_out + n) = v;
+      } else if (args.out_dtype == FMOE_BF16) {
+        uint2 u;
+        u.x = pack2(v[0], v[1]);
+        u.y = pack2(v[2], v[3]);
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(base) + orow + n) = u;
+      } else {
+        *reinterpret_cast<f32x4*>(static_cast<float*>(base) + orow + n) = v;
+      }
+    }
+  }
+}
+
 // Adds the chunk partials of each multi-chunk group in chunk order; 8
 // consecutive outputs per thread (m_out * n_out is a multiple of 64).
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const WgradArgs args) {
@@ -973,11 +1163,10 @@ extern "C" int fmoe_weight_grad(const void* a_routed, const void* a_shared, int6
     a.out_lo[g] = out_lo[g];
     a.out_hi[g] = (m_split < m_out) ? out_hi[g] : nullptr;
   }
-  using C = CfgWgrad;
-  const int64_t tiles = ceil_div(m_out, C::BM) * ceil_div(n_out, C::BN);
+  const int64_t tiles = ceil_div(m_out, core::BM) * ceil_div(n_out, core::BN);
   const int64_t max_chunks = (rows_routed + rows_shared) / a.kc + G;
   hipStream_t s = as_stream(stream);
-  wgrad_kernel<C><<<dim3(max_chunks * tiles), dim3(C::NT), 0, s>>>(a);
+  wgrad_tr_kernel<<<dim3(max_chunks * tiles), dim3(core::NT), 0, s>>>(a, offsets);
   const int64_t mn = m_out * n_out;
   wgrad_reduce_kernel<<<dim3(ceil_div(mn, 256 * 8), G), dim3(256), 0, s>>>(a);
   return launch_status();
