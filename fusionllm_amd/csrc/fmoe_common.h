@@ -79,9 +79,9 @@ __device__ __forceinline__ float fm_expf(float x) {
 __device__ __forceinline__ float fm_sigmoid(float l) { return 1.0f / (1.0f + fm_expf(-l)); }
 
 // Fast sigmoid for the SwiGLU epilogues (the result is rounded to bf16, so a
-// few fp32 ulps do not matter): v_exp_f32 computes 2^x.
+// few fp32 ulps do not matter): v_exp_f32 computes 2^x, v_rcp_f32 1/x (1 ulp).
 __device__ __forceinline__ float fast_sigmoid(float a) {
-  return 1.0f / (1.0f + __builtin_amdgcn_exp2f(-a * 1.4426950408889634f));
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-a * 1.4426950408889634f));
 }
 
 // Top-k order: a beats b if a is NaN and b is not, or a > b.  Scanning experts
