@@ -126,14 +126,22 @@ def gateup_fwd(x_perm, x_shared, offsets, n_experts: int, w1s, w3s, inter: int):
     return ab, h
 
 
+def _split_workspace(dev):
+    """fp32 workspace for the K-split last round of the plain-output products."""
+    lib = _lib.load()
+    nbytes = lib.fmoe_split_workspace_bytes()
+    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev), nbytes
+
+
 @_timed
 def down_fwd(h, offsets, n_experts: int, rows_routed: int, rows_shared: int, w2s, dim: int):
     lib = _lib.load()
     rows, inter = h.shape
     out = torch.empty(rows, dim, dtype=torch.bfloat16, device=h.device)
+    ws, ws_bytes = _split_workspace(h.device)
     check(lib.fmoe_down_fwd(_req(h, "h", torch.bfloat16), _req(offsets, "offsets", torch.int32), n_experts,
                             rows_routed, rows_shared, dim, inter, ptr_array([w.data_ptr() for w in w2s]),
-                            out.data_ptr(), _stream()),
+                            out.data_ptr(), ws.data_ptr(), ws_bytes, _stream()),
           "fmoe_down_fwd")
     return out
 
@@ -212,9 +220,11 @@ def gateup_bwd_dx(d_ab, offsets, n_experts: int, rows_routed: int, rows_shared: 
     if tuple(w13t.shape) != (G, dim, two_i):
         raise RuntimeError(f"w13t must be {(G, dim, two_i)} (got {tuple(w13t.shape)})")
     dx_rows = torch.empty(rows, dim, dtype=torch.bfloat16, device=d_ab.device)
+    ws, ws_bytes = _split_workspace(d_ab.device)
     check(lib.fmoe_gateup_bwd_dx(_req(d_ab, "d_ab", torch.bfloat16), _req(offsets, "offsets", torch.int32),
                                  n_experts, rows_routed, rows_shared, dim, two_i // 2,
-                                 _req(w13t, "w13t", torch.bfloat16), dx_rows.data_ptr(), _stream()),
+                                 _req(w13t, "w13t", torch.bfloat16), dx_rows.data_ptr(),
+                                 ws.data_ptr(), ws_bytes, _stream()),
           "fmoe_gateup_bwd_dx")
     return dx_rows
 

@@ -174,6 +174,7 @@ struct GemmArgs {
   const uint16_t* b0[FMOE_MAX_EXPERTS + 1];  // w1 / w2 / w2t / w13t
   const uint16_t* b1[FMOE_MAX_EXPERTS + 1];  // w3 (GATEUP_FWD only)
   int small_max;  // groups with 1 .. small_max rows go to small_gemm_kernel (0: none)
+  float* split_ws;  // DOWN_FWD / GATEUP_BWD: fp32 partials of K-split tiles (nullptr: no split)
 };
 
 // ---- tiled row-grouped kernel ----------------------------------------------
@@ -236,6 +237,50 @@ constexpr int epi_stores() {
   return MODE == GATEUP_FWD ? 24 : (MODE == DOWN_BWD ? 32 : 16);
 }
 
+// K-split of the last, partial round of tiles (plain-output products only).
+// With T tiles on P workgroups, the T mod P tiles of the last round would run
+// on a fraction of the CUs; instead each is split into S K ranges (S <= 4,
+// R * S <= P, at least 4 K steps per range) whose fp32 partials
+// split_reduce_kernel adds in range order.  Work items: tiles 0 .. full-1 whole,
+// then R * S ranges.
+struct SplitPlan {
+  int full, R, S;
+  __device__ __forceinline__ int items() const { return full + R * S; }
+};
+template <int MODE>
+__device__ __forceinline__ SplitPlan split_plan(const GemmArgs& a, int T, int P, int nk) {
+  SplitPlan sp{T, 0, 1};
+  if constexpr (MODE == DOWN_FWD || MODE == GATEUP_BWD) {
+    if (a.split_ws == nullptr || T <= 0) return sp;
+    const int R = T % P;
+    if (R == 0) return sp;
+    int S = min(P / R, 4);
+    S = min(S, nk / 4);
+    if (S < 2) return sp;
+    sp.full = T - R;
+    sp.R = R;
+    sp.S = S;
+  }
+  return sp;
+}
+// Work item -> tile, first K step, K steps, partial slot (-1: whole tile).
+__device__ __forceinline__ void split_item(const SplitPlan& sp, int nk, int item, int& tile, int& k0, int& kn,
+                                           int& slot) {
+  if (item < sp.full) {
+    tile = item;
+    k0 = 0;
+    kn = nk;
+    slot = -1;
+  } else {
+    const int j = item - sp.full;
+    const int s = j % sp.S;
+    tile = sp.full + j / sp.S;
+    k0 = s * nk / sp.S;
+    kn = (s + 1) * nk / sp.S - k0;
+    slot = j;
+  }
+}
+
 template <int MODE>
 __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs args,
                                                                  const int32_t* __restrict__ offsets) {
@@ -250,11 +295,17 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
   constexpr int TN_COLS = (MODE == GATEUP_FWD) ? BN / 2 : BN;
   const int tiles_n = (args.N + TN_COLS - 1) / TN_COLS;
   const int total_tiles = count_tiles(args, offsets, tiles_n);
-  const int my_tiles = (total_tiles - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) /
-                       static_cast<int>(gridDim.x);
-  if (my_tiles <= 0) return;
+  const int NP = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
   const int nk = args.K / BK;
-  const int total = my_tiles * nk;  // K steps of 64 over all of this workgroup's tiles
+  const SplitPlan sp = split_plan<MODE>(args, total_tiles, NP, nk);
+  const int my_items = (sp.items() - b + NP - 1) / NP;  // items b, b + NP, ...
+  if (my_items <= 0) return;
+  int total = 0;  // K steps of 64 over all of this workgroup's items
+  for (int i = 0; i < my_items; ++i) {
+    int t_, k0_, kn_, s_;
+    split_item(sp, nk, b + i * NP, t_, k0_, kn_, s_);
+    total += kn_;
+  }
 
   // ---- global -> LDS copy cursor
   // Copy instruction i of wave w writes LDS rows 64 i + 8 w .. +7 of an operand;
@@ -262,15 +313,16 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
   const int drow = w * 8 + (lane >> 3);
   const int dchunk = (lane & 7) ^ swz(drow);  // swz(64 i + drow) == swz(drow)
   const uint32_t lds_copy = sbase + w * 1024;
-  int c_ti = 0, c_kt = 0;
+  int c_ti = 0, c_kt = 0, c_k0 = 0, c_kn = 0;  // item ordinal, step within it, its K range
   const uint16_t* c_a = nullptr;   // A rows of the tile being copied
   const uint16_t* c_b0 = nullptr;  // B operand base(s)
   const uint16_t* c_b1 = nullptr;
   int c_last_row = 0, c_n0 = 0;    // last valid A row of the tile, first B row
   auto copy_tile = [&](int ti) {
+    int tile, slot;
+    split_item(sp, nk, b + ti * NP, tile, c_k0, c_kn, slot);
     int g, tm, tn, row_base, M;
-    locate_tile(args, offsets, tiles_n, static_cast<int>(blockIdx.x) + ti * static_cast<int>(gridDim.x), g, tm, tn, row_base,
-                M);
+    locate_tile(args, offsets, tiles_n, tile, g, tm, tn, row_base, M);
     const uint16_t* A = (g < args.E || args.a_shared == nullptr) ? args.a_routed + static_cast<int64_t>(row_base) * args.lda
                                                                  : args.a_shared;
     c_a = A + static_cast<int64_t>(tm) * BM * args.lda;
@@ -283,7 +335,7 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
   const int lda = static_cast<int>(args.lda), ldb = static_cast<int>(args.ldb);
   auto issue = [&](int it) {
     const uint32_t st = lds_copy + (it & 1) * STAGE;
-    const int kofs = c_kt * BK;
+    const int kofs = (c_k0 + c_kt) * BK;
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
       const int r = min(64 * i + drow, c_last_row);
@@ -296,9 +348,9 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
       const uint16_t* b = (MODE == GATEUP_FWD && (i & 1)) ? c_b1 : c_b0;
       copy16(st + A_BYTES + i * 8192, b + kofs, static_cast<uint32_t>(n * ldb + dchunk * 8) * 2u);
     }
-    if (++c_kt == nk) {
+    if (++c_kt == c_kn) {
       c_kt = 0;
-      if (++c_ti < my_tiles) copy_tile(c_ti);
+      if (++c_ti < my_items) copy_tile(c_ti);
     }
   };
 
@@ -327,7 +379,11 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   uint8_t* ep = smem + 2 * STAGE + w * EPI;  // this wave's epilogue staging (4 KB)
-  int e_ti = 0, e_kt = 0;
+  int e_ti = 0, e_kt = 0, e_kn = c_kn, e_slot = -1, e_tile = 0;
+  {
+    int k0_;
+    split_item(sp, nk, b, e_tile, k0_, e_kn, e_slot);
+  }
   int last_epi = -4;        // iteration whose end wrote an epilogue
   bool last_full = false;   // that epilogue issued exactly epi_stores<MODE>() stores
   for (int it = 0; it < total; ++it) {
@@ -349,7 +405,7 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
     }
     kstep<0>(acc, P, Q[1], Q[0], xa, xb, src);
 
-    if (++e_kt < nk) continue;
+    if (++e_kt < e_kn) continue;
     // ---- tile epilogue: this wave's 64 x 128 block
     e_kt = 0;
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3\n" ::: "memory");  // MFMA results -> VALU reads
@@ -357,110 +413,152 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
     // from being hoisted out of the main loop (where it would occupy registers)
     int el = lane;
     asm volatile("" : "+v"(el));
-    int g, tm, tn, row_base, M;
-    locate_tile(args, offsets, tiles_n, static_cast<int>(blockIdx.x) + e_ti * static_cast<int>(gridDim.x), g, tm, tn,
-                row_base, M);
-    const int rows_valid = min(M - tm * BM, BM);
-    const int col0 = tn * TN_COLS + wn * (TN_COLS / WN);  // first output column of this wave
-    const bool full = rows_valid == BM && (tn + 1) * TN_COLS <= args.N;
-    const int64_t grow0 = static_cast<int64_t>(row_base) + tm * BM + wm * WTM;
+    if (e_slot >= 0) {
+      // K-split range: fp32 partial of the 256 x 256 tile (local row-major)
+      float* part = args.split_ws + static_cast<int64_t>(e_slot) * BM * BN;
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      // stage rows 16 i .. 16 i + 15 of the wave block, 128 accumulator columns
-      // (256 bytes per row; chunk c of row r at slot c ^ r)
-      {
-        const int r = el & 15;
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int col = j * 16 + (el >> 4) * 4;
-          const uint32_t off = r * 256 + ((((col >> 3) ^ r)) << 4) + (col & 7) * 2;
-          uint2 v;
-          v.x = pack2(acc[i][j][0], acc[i][j][1]);
-          v.y = pack2(acc[i][j][2], acc[i][j][3]);
-          *reinterpret_cast<uint2*>(ep + off) = v;
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int r = t * 4 + (el >> 4), c = el & 15;
-        const uint4 v = *reinterpret_cast<const uint4*>(ep + r * 256 + ((c ^ r) << 4));
-        const int lrow = wm * WTM + i * 16 + r;
-        const int64_t grow = grow0 + i * 16 + r;
-        if constexpr (MODE == GATEUP_FWD) {
-          // columns 0..63: a, 64..127: b for h columns col0 .. col0 + 63
-          const int hc = col0 + (c & 7) * 8;
-          if (full || (lrow < rows_valid && hc < args.N)) {
-            uint16_t* dst = args.c0 + grow * args.ldc0 + (c < 8 ? 0 : args.inter) + hc;
-            *reinterpret_cast<uint4*>(dst) = v;
+        for (int j = 0; j < FN; ++j)
+          *reinterpret_cast<f32x4*>(part + (wm * WTM + i * 16 + (el & 15)) * BN + wn * WTN + j * 16 + (el >> 4) * 4) =
+              acc[i][j];
+    } else {
+      int g, tm, tn, row_base, M;
+      locate_tile(args, offsets, tiles_n, e_tile, g, tm, tn, row_base, M);
+      const int rows_valid = min(M - tm * BM, BM);
+      const int col0 = tn * TN_COLS + wn * (TN_COLS / WN);  // first output column of this wave
+      const bool full = rows_valid == BM && (tn + 1) * TN_COLS <= args.N;
+      const int64_t grow0 = static_cast<int64_t>(row_base) + tm * BM + wm * WTM;
+  #pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        // stage rows 16 i .. 16 i + 15 of the wave block, 128 accumulator columns
+        // (256 bytes per row; chunk c of row r at slot c ^ r)
+        {
+          const int r = el & 15;
+  #pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            const int col = j * 16 + (el >> 4) * 4;
+            const uint32_t off = r * 256 + ((((col >> 3) ^ r)) << 4) + (col & 7) * 2;
+            uint2 v;
+            v.x = pack2(acc[i][j][0], acc[i][j][1]);
+            v.y = pack2(acc[i][j][2], acc[i][j][3]);
+            *reinterpret_cast<uint2*>(ep + off) = v;
           }
-        } else if constexpr (MODE == DOWN_BWD) {
-          // h = s * b, s = bf16(silu(a)); dh arrives bf16-rounded:
-          // da = bf16(bf16(dh * b) * silu'(a)), db = bf16(dh * s)
-          const int hc = col0 + c * 8;
-          if (full || (lrow < rows_valid && hc < args.N)) {
-            const uint4 avv = *reinterpret_cast<const uint4*>(args.aux + grow * args.ldaux + hc);
-            const uint4 bvv = *reinterpret_cast<const uint4*>(args.aux + grow * args.ldaux + args.inter + hc);
-            float dh[8], af[8], bfv[8], da[8], db[8];
-            unpack8(v, dh);
-            unpack8(avv, af);
-            unpack8(bvv, bfv);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const float sg = fast_sigmoid(af[e]);
-              const float sv = bf_round(af[e] * sg);
-              const float ds = bf_round(dh[e] * bfv[e]);
-              da[e] = ds * (sg * (1.0f + af[e] * (1.0f - sg)));
-              db[e] = dh[e] * sv;
+        }
+  #pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int r = t * 4 + (el >> 4), c = el & 15;
+          const uint4 v = *reinterpret_cast<const uint4*>(ep + r * 256 + ((c ^ r) << 4));
+          const int lrow = wm * WTM + i * 16 + r;
+          const int64_t grow = grow0 + i * 16 + r;
+          if constexpr (MODE == GATEUP_FWD) {
+            // columns 0..63: a, 64..127: b for h columns col0 .. col0 + 63
+            const int hc = col0 + (c & 7) * 8;
+            if (full || (lrow < rows_valid && hc < args.N)) {
+              uint16_t* dst = args.c0 + grow * args.ldc0 + (c < 8 ? 0 : args.inter) + hc;
+              *reinterpret_cast<uint4*>(dst) = v;
             }
-            *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + hc) = pack8(da);
-            *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + args.inter + hc) = pack8(db);
+          } else if constexpr (MODE == DOWN_BWD) {
+            // h = s * b, s = bf16(silu(a)); dh arrives bf16-rounded:
+            // da = bf16(bf16(dh * b) * silu'(a)), db = bf16(dh * s)
+            const int hc = col0 + c * 8;
+            if (full || (lrow < rows_valid && hc < args.N)) {
+              const uint4 avv = *reinterpret_cast<const uint4*>(args.aux + grow * args.ldaux + hc);
+              const uint4 bvv = *reinterpret_cast<const uint4*>(args.aux + grow * args.ldaux + args.inter + hc);
+              float dh[8], af[8], bfv[8], da[8], db[8];
+              unpack8(v, dh);
+              unpack8(avv, af);
+              unpack8(bvv, bfv);
+  #pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const float sg = fast_sigmoid(af[e]);
+                const float sv = bf_round(af[e] * sg);
+                const float ds = bf_round(dh[e] * bfv[e]);
+                da[e] = ds * (sg * (1.0f + af[e] * (1.0f - sg)));
+                db[e] = dh[e] * sv;
+              }
+              *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + hc) = pack8(da);
+              *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + args.inter + hc) = pack8(db);
+            }
+          } else {
+            const int oc = col0 + c * 8;
+            if (full || (lrow < rows_valid && oc < args.N))
+              *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + oc) = v;
           }
-        } else {
-          const int oc = col0 + c * 8;
-          if (full || (lrow < rows_valid && oc < args.N))
-            *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + oc) = v;
+        }
+        if constexpr (MODE == GATEUP_FWD) {
+          // h = bf16(bf16(silu(a)) * b) for the 16 rows x 64 h columns, staged as
+          // 128-byte rows (chunk c of row r at slot c ^ swz(r))
+          const int r = el & 15;
+  #pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float hv[4];
+  #pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float a = bf_round(acc[i][j][e]);
+              const float b = bf_round(acc[i][j + 4][e]);
+              hv[e] = bf_round(a * fast_sigmoid(a)) * b;
+            }
+            const int col = j * 16 + (el >> 4) * 4;
+            const uint32_t off = r * 128 + ((((col >> 3) ^ swz(r))) << 4) + (col & 7) * 2;
+            uint2 v;
+            v.x = pack2(hv[0], hv[1]);
+            v.y = pack2(hv[2], hv[3]);
+            *reinterpret_cast<uint2*>(ep + off) = v;
+          }
+  #pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int rr = t * 8 + (el >> 3), c = el & 7;
+            const uint4 v = *reinterpret_cast<const uint4*>(ep + rr * 128 + ((c ^ swz(rr)) << 4));
+            const int lrow = wm * WTM + i * 16 + rr;
+            const int hc = col0 + c * 8;
+            if (full || (lrow < rows_valid && hc < args.N))
+              *reinterpret_cast<uint4*>(args.c1 + (grow0 + i * 16 + rr) * args.ldc1 + hc) = v;
+          }
         }
       }
-      if constexpr (MODE == GATEUP_FWD) {
-        // h = bf16(bf16(silu(a)) * b) for the 16 rows x 64 h columns, staged as
-        // 128-byte rows (chunk c of row r at slot c ^ swz(r))
-        const int r = el & 15;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float hv[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float a = bf_round(acc[i][j][e]);
-            const float b = bf_round(acc[i][j + 4][e]);
-            hv[e] = bf_round(a * fast_sigmoid(a)) * b;
-          }
-          const int col = j * 16 + (el >> 4) * 4;
-          const uint32_t off = r * 128 + ((((col >> 3) ^ swz(r))) << 4) + (col & 7) * 2;
-          uint2 v;
-          v.x = pack2(hv[0], hv[1]);
-          v.y = pack2(hv[2], hv[3]);
-          *reinterpret_cast<uint2*>(ep + off) = v;
-        }
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int rr = t * 8 + (el >> 3), c = el & 7;
-          const uint4 v = *reinterpret_cast<const uint4*>(ep + rr * 128 + ((c ^ swz(rr)) << 4));
-          const int lrow = wm * WTM + i * 16 + rr;
-          const int hc = col0 + c * 8;
-          if (full || (lrow < rows_valid && hc < args.N))
-            *reinterpret_cast<uint4*>(args.c1 + (grow0 + i * 16 + rr) * args.ldc1 + hc) = v;
-        }
-      }
-    }
+      last_full = full;
+    }  // whole tile
+    if (e_slot >= 0) last_full = false;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     asm volatile("s_nop 1" ::: "memory");  // VALU writes -> MFMA reads of the accumulators
     last_epi = it;
-    last_full = full;
-    ++e_ti;
+    if (++e_ti < my_items) {
+      int k0_;
+      split_item(sp, nk, b + e_ti * NP, e_tile, k0_, e_kn, e_slot);
+    }
   }
+}
+
+// Sums the S fp32 partials of every K-split tile in range order and writes the
+// bf16 tile.  Block = (split tile r, 2048 outputs); P = the product's grid size.
+template <int MODE>
+__global__ __launch_bounds__(256) void split_reduce_kernel(const GemmArgs args, const int32_t* __restrict__ offsets,
+                                                           int P) {
+  using namespace core;
+  const int tiles_n = (args.N + BN - 1) / BN;
+  const int T = count_tiles(args, offsets, tiles_n);
+  const SplitPlan sp = split_plan<MODE>(args, T, P, args.K / BK);
+  const int r = blockIdx.x / 32;
+  if (r >= sp.R) return;
+  const int e0 = (blockIdx.x % 32) * 2048 + threadIdx.x * 8;
+  const int row = e0 / BN, col = e0 % BN;
+  int g, tm, tn, row_base, M;
+  locate_tile(args, offsets, tiles_n, sp.full + r, g, tm, tn, row_base, M);
+  if (row >= M - tm * BM || tn * BN + col >= args.N) return;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int s = 0; s < sp.S; ++s) {
+    const float4* src =
+        reinterpret_cast<const float4*>(args.split_ws + static_cast<int64_t>(r * sp.S + s) * BM * BN + e0);
+    const float4 u = src[0], v = src[1];
+    acc[0] = acc[0] + u.x; acc[1] = acc[1] + u.y; acc[2] = acc[2] + u.z; acc[3] = acc[3] + u.w;
+    acc[4] = acc[4] + v.x; acc[5] = acc[5] + v.y; acc[6] = acc[6] + v.z; acc[7] = acc[7] + v.w;
+  }
+  const int64_t grow = static_cast<int64_t>(row_base) + tm * BM + row;
+  *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + tn * BN + col) = pack8(acc);
 }
 
 // ---- small groups (decode-sized batches) -------------------------------------
@@ -969,6 +1067,10 @@ int launch_rows(GemmArgs& a, int64_t rows_routed, int64_t rows_shared, int E, vo
   if (tiles <= 0) return FMOE_OK;
   const int64_t grid = tiles < device_cus() ? tiles : device_cus();
   rows_gemm_kernel<MODE><<<dim3(grid), dim3(core::NT), 0, as_stream(stream)>>>(a, a.offsets);
+  if constexpr (MODE == DOWN_FWD || MODE == GATEUP_BWD) {
+    if (a.split_ws != nullptr)
+      split_reduce_kernel<MODE><<<dim3(grid * 32), dim3(256), 0, as_stream(stream)>>>(a, a.offsets, static_cast<int>(grid));
+  }
   if constexpr (kHasSmall) {
     if (a.small_max > 0) {
       const int G = E + (rows_shared > 0 ? 1 : 0);
@@ -1023,9 +1125,14 @@ extern "C" int fmoe_gateup_fwd(const void* x_routed, const void* x_shared, const
   return launch_rows<GATEUP_FWD>(a, rows_routed, rows_shared, n_experts, stream);
 }
 
+extern "C" size_t fmoe_split_workspace_bytes(void) {
+  return static_cast<size_t>(device_cus()) * core::BM * core::BN * sizeof(float);
+}
+
 extern "C" int fmoe_down_fwd(const void* h, const int32_t* offsets, int n_experts,
                              int64_t rows_routed, int64_t rows_shared, int64_t dim, int64_t inter,
-                             const void* const* w2, void* out, void* stream) {
+                             const void* const* w2, void* out, void* workspace, size_t workspace_bytes,
+                             void* stream) {
   int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
   if (st) return st;
   if (rows_routed + rows_shared == 0) return FMOE_OK;
@@ -1042,6 +1149,7 @@ extern "C" int fmoe_down_fwd(const void* h, const int32_t* offsets, int n_expert
   a.ldb = inter;
   a.c0 = static_cast<uint16_t*>(out);
   a.ldc0 = dim;
+  a.split_ws = (workspace && workspace_bytes >= fmoe_split_workspace_bytes()) ? static_cast<float*>(workspace) : nullptr;
   const int G = n_experts + (rows_shared > 0 ? 1 : 0);
   for (int g = 0; g < G; ++g) {
     if (!w2[g]) return FMOE_ERR_INVALID_ARG;
@@ -1081,7 +1189,8 @@ extern "C" int fmoe_down_bwd_dx(const void* d_out_routed, const void* d_out_shar
 
 extern "C" int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int n_experts,
                                   int64_t rows_routed, int64_t rows_shared, int64_t dim,
-                                  int64_t inter, const void* w13t, void* dx_rows, void* stream) {
+                                  int64_t inter, const void* w13t, void* dx_rows, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
   int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
   if (st) return st;
   if (rows_routed + rows_shared == 0) return FMOE_OK;
@@ -1098,6 +1207,7 @@ extern "C" int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int 
   a.ldb = 2 * inter;  // w13t[g] is [dim, 2*inter]: row n = dim index, K = 2*inter contiguous
   a.c0 = static_cast<uint16_t*>(dx_rows);
   a.ldc0 = dim;
+  a.split_ws = (workspace && workspace_bytes >= fmoe_split_workspace_bytes()) ? static_cast<float*>(workspace) : nullptr;
   const int G = n_experts + (rows_shared > 0 ? 1 : 0);
   for (int g = 0; g < G; ++g)
     a.b0[g] = static_cast<const uint16_t*>(w13t) + static_cast<int64_t>(g) * dim * 2 * inter;

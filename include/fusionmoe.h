@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define FMOE_ABI_VERSION 2
+#define FMOE_ABI_VERSION 3
 #define FMOE_MAX_EXPERTS 64
 #define FMOE_MAX_TOPK 8
 
@@ -119,13 +119,20 @@ int fmoe_gateup_fwd(const void* x_routed, const void* x_shared,
                     const void* const* w1, const void* const* w3,
                     void* ab, void* h, void* stream);
 
+/* Workspace of the plain-output products (fmoe_down_fwd, fmoe_gateup_bwd_dx)
+ * for the current device: fp32 partials of the tiles of the last, partial
+ * round of the persistent grid, which are split along K (up to 4 ranges) and
+ * summed in range order (deterministic).  Passing no (or a smaller) workspace
+ * runs those tiles whole. */
+size_t fmoe_split_workspace_bytes(void);
+
 /* Grouped down projection w2(h) of SwiGLUExpert.forward (models/moe.py:21),
  * all experts plus the shared expert in one launch.  h: [rows, inter];
- * out: [rows, dim] bf16. */
+ * out: [rows, dim] bf16; workspace: see fmoe_split_workspace_bytes. */
 int fmoe_down_fwd(const void* h, const int32_t* offsets, int n_experts,
                   int64_t rows_routed, int64_t rows_shared,
                   int64_t dim, int64_t inter, const void* const* w2,
-                  void* out, void* stream);
+                  void* out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Weighted combine fused with the shared-expert add.  Replaces
@@ -176,11 +183,11 @@ int fmoe_down_bwd_dx(const void* d_out_routed, const void* d_out_shared,
                      const void* ab, void* d_ab, void* stream);
 
 /* dx_rows = da w1 + db w3 for every row (one product over K = 2*inter);
- * dx_rows: [rows, dim] bf16. */
+ * dx_rows: [rows, dim] bf16; workspace: see fmoe_split_workspace_bytes. */
 int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int n_experts,
                        int64_t rows_routed, int64_t rows_shared,
                        int64_t dim, int64_t inter, const void* w13t,
-                       void* dx_rows, void* stream);
+                       void* dx_rows, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Grouped weight gradient, the dW half of nn.Linear backward for every expert:
  *   G_e = A_e^T B_e,  A_e = rows of expert e of A ([*, m_out]),

@@ -21,7 +21,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     syms = declared_symbols()
-    assert len(syms) == 17
+    assert len(syms) == 18
     for s in syms:
         assert hasattr(lib, s), s
     assert set(syms) == set(_lib.SIGNATURES), "ctypes binding and header disagree"
