@@ -45,7 +45,24 @@ def parse():
     p.add_argument("--cpu-tokens", type=int, default=2048, help="token sample for the CPU baseline")
     p.add_argument("--fwd-only", action="store_true",
                    help="time the forward pass alone (decode-shaped C3 configs); not the headline metric")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="run only a device-to-device copy of COPY_BYTES (3 times): the known-size kernel whose "
+                        "FETCH_SIZE / WRITE_SIZE counters scale the GEMM counters to HBM bytes")
     return p.parse_args()
+
+
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration():
+    dev = torch.device("cuda:0")
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "copies": 3}), flush=True)
 
 
 def kernel_model(cfg, T):
@@ -116,6 +133,9 @@ def cpu_baseline(cfg, data, n_tokens):
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only (one MI355X per box); "
                                    "run without --gpus or with --gpus 1"}))

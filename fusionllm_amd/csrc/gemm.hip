@@ -263,6 +263,15 @@ __device__ __forceinline__ SplitPlan split_plan(const GemmArgs& a, int T, int P,
   }
   return sp;
 }
+// Workgroup b runs on XCD b % 8 (round-robin dispatch over the 8 XCDs of an
+// MI355X, each with its own L2).  Item i of round r of workgroup b is
+// r * P + xcd_slot(b): the workgroups of one XCD take a contiguous range of
+// items, so the tiles that share operand rows (consecutive n tiles of one m
+// tile) meet in the same L2.
+__device__ __forceinline__ int xcd_slot(int b, int P) {
+  return (P % 8 == 0) ? (b % 8) * (P / 8) + b / 8 : b;
+}
+
 // Work item -> tile, first K step, K steps, partial slot (-1: whole tile).
 __device__ __forceinline__ void split_item(const SplitPlan& sp, int nk, int item, int& tile, int& k0, int& kn,
                                            int& slot) {
@@ -295,7 +304,7 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
   constexpr int TN_COLS = (MODE == GATEUP_FWD) ? BN / 2 : BN;
   const int tiles_n = (args.N + TN_COLS - 1) / TN_COLS;
   const int total_tiles = count_tiles(args, offsets, tiles_n);
-  const int NP = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
+  const int NP = static_cast<int>(gridDim.x), b = xcd_slot(static_cast<int>(blockIdx.x), NP);
   const int nk = args.K / BK;
   const SplitPlan sp = split_plan<MODE>(args, total_tiles, NP, nk);
   const int my_items = (sp.items() - b + NP - 1) / NP;  // items b, b + NP, ...
@@ -839,7 +848,9 @@ __global__ __launch_bounds__(core::NT, 1) void wgrad_tr_kernel(const WgradArgs a
   const int tiles = tiles_m * tiles_n;
   const int G = args.E + (args.rows_shared > 0 ? 1 : 0);
 
-  // ---- work unit -> (group, K chunk, output tile)
+  // ---- work unit -> (group, K chunk, output tile).  Units are dispatched in
+  // order (largest groups' chunks first when they come first); the hardware
+  // hands the next unit to the next free CU, which balances the uneven units.
   int unit = blockIdx.x;
   int g = 0, row_base = 0, M = 0, chunks = 0, pbase = 0;
   for (; g < G; ++g) {
