@@ -307,6 +307,19 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
   const int NP = static_cast<int>(gridDim.x), b = xcd_slot(static_cast<int>(blockIdx.x), NP);
   const int nk = args.K / BK;
   const SplitPlan sp = split_plan<MODE>(args, total_tiles, NP, nk);
+  if constexpr (MODE == DOWN_FWD || MODE == GATEUP_BWD) {
+    // descriptors of the split tiles for split_reduce_kernel (after the partials)
+    if (args.split_ws != nullptr && threadIdx.x == 0) {
+      int4* hdr = reinterpret_cast<int4*>(args.split_ws + static_cast<int64_t>(NP) * BM * BN);
+      const int r = static_cast<int>(blockIdx.x);
+      if (r == 0) hdr[0] = make_int4(sp.R, sp.S, 0, 0);
+      if (r < sp.R) {
+        int g, tm, tn, row_base, M;
+        locate_tile(args, offsets, tiles_n, sp.full + r, g, tm, tn, row_base, M);
+        hdr[1 + r] = make_int4(row_base + tm * BM, min(M - tm * BM, BM), tn * BN, min(args.N - tn * BN, BN));
+      }
+    }
+  }
   const int my_items = (sp.items() - b + NP - 1) / NP;  // items b, b + NP, ...
   if (my_items <= 0) return;
   int total = 0;  // K steps of 64 over all of this workgroup's items
@@ -543,31 +556,32 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
 }
 
 // Sums the S fp32 partials of every K-split tile in range order and writes the
-// bf16 tile.  Block = (split tile r, 2048 outputs); P = the product's grid size.
-template <int MODE>
-__global__ __launch_bounds__(256) void split_reduce_kernel(const GemmArgs args, const int32_t* __restrict__ offsets,
-                                                           int P) {
+// bf16 tile.  The product wrote, after the P tiles of partials, a header
+// {R, S} and one descriptor {first row, valid rows, first column, valid
+// columns} per split tile.  Block = (split tile r, eighth of its rows).
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ ws, int P,
+                                                           uint16_t* __restrict__ out, int64_t ldo) {
   using namespace core;
-  const int tiles_n = (args.N + BN - 1) / BN;
-  const int T = count_tiles(args, offsets, tiles_n);
-  const SplitPlan sp = split_plan<MODE>(args, T, P, args.K / BK);
-  const int r = blockIdx.x / 32;
-  if (r >= sp.R) return;
-  const int e0 = (blockIdx.x % 32) * 2048 + threadIdx.x * 8;
-  const int row = e0 / BN, col = e0 % BN;
-  int g, tm, tn, row_base, M;
-  locate_tile(args, offsets, tiles_n, sp.full + r, g, tm, tn, row_base, M);
-  if (row >= M - tm * BM || tn * BN + col >= args.N) return;
-  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int s = 0; s < sp.S; ++s) {
-    const float4* src =
-        reinterpret_cast<const float4*>(args.split_ws + static_cast<int64_t>(r * sp.S + s) * BM * BN + e0);
-    const float4 u = src[0], v = src[1];
-    acc[0] = acc[0] + u.x; acc[1] = acc[1] + u.y; acc[2] = acc[2] + u.z; acc[3] = acc[3] + u.w;
-    acc[4] = acc[4] + v.x; acc[5] = acc[5] + v.y; acc[6] = acc[6] + v.z; acc[7] = acc[7] + v.w;
+  const int4* hdr = reinterpret_cast<const int4*>(ws + static_cast<int64_t>(P) * BM * BN);
+  const int4 h0 = hdr[0];
+  const int r = blockIdx.x / 8, part = blockIdx.x % 8;
+  if (r >= h0.x) return;
+  const int S = h0.y;
+  const int4 d = hdr[1 + r];
+  const float* src0 = ws + static_cast<int64_t>(r) * S * BM * BN;
+  // rows 32 part .. 32 part + 31 of the tile: 8192 outputs, 8 per thread and pass
+  for (int e0 = part * 32 * BN + threadIdx.x * 8; e0 < (part + 1) * 32 * BN; e0 += 256 * 8) {
+    const int row = e0 / BN, col = e0 % BN;
+    if (row >= d.y || col >= d.w) continue;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int s = 0; s < S; ++s) {
+      const float4* src = reinterpret_cast<const float4*>(src0 + static_cast<int64_t>(s) * BM * BN + e0);
+      const float4 u = src[0], v = src[1];
+      acc[0] = acc[0] + u.x; acc[1] = acc[1] + u.y; acc[2] = acc[2] + u.z; acc[3] = acc[3] + u.w;
+      acc[4] = acc[4] + v.x; acc[5] = acc[5] + v.y; acc[6] = acc[6] + v.z; acc[7] = acc[7] + v.w;
+    }
+    *reinterpret_cast<uint4*>(out + static_cast<int64_t>(d.x + row) * ldo + d.z + col) = pack8(acc);
   }
-  const int64_t grow = static_cast<int64_t>(row_base) + tm * BM + row;
-  *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + tn * BN + col) = pack8(acc);
 }
 
 // ---- small groups (decode-sized batches) -------------------------------------
@@ -1080,7 +1094,8 @@ int launch_rows(GemmArgs& a, int64_t rows_routed, int64_t rows_shared, int E, vo
   rows_gemm_kernel<MODE><<<dim3(grid), dim3(core::NT), 0, as_stream(stream)>>>(a, a.offsets);
   if constexpr (MODE == DOWN_FWD || MODE == GATEUP_BWD) {
     if (a.split_ws != nullptr)
-      split_reduce_kernel<MODE><<<dim3(grid * 32), dim3(256), 0, as_stream(stream)>>>(a, a.offsets, static_cast<int>(grid));
+      split_reduce_kernel<<<dim3(grid * 8), dim3(256), 0, as_stream(stream)>>>(a.split_ws, static_cast<int>(grid),
+                                                                               a.c0, a.ldc0);
   }
   if constexpr (kHasSmall) {
     if (a.small_max > 0) {
@@ -1137,7 +1152,8 @@ extern "C" int fmoe_gateup_fwd(const void* x_routed, const void* x_shared, const
 }
 
 extern "C" size_t fmoe_split_workspace_bytes(void) {
-  return static_cast<size_t>(device_cus()) * core::BM * core::BN * sizeof(float);
+  const size_t P = static_cast<size_t>(device_cus());
+  return P * core::BM * core::BN * sizeof(float) + (P + 1) * 16;  // partials + descriptors
 }
 
 extern "C" int fmoe_down_fwd(const void* h, const int32_t* offsets, int n_experts,
