@@ -89,6 +89,26 @@ def kernel_model(cfg, T):
     }
 
 
+def hbm_traffic(cfg_name, entry):
+    """HBM bytes per launch of an entry point from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE readings (profiles/hbm_counters_c2.json), each
+    counter scaled by what it read for a device copy of known size; None when
+    no reading covers this workload and entry point."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_counters_c2.json")
+    if not cfg_name.startswith("C2") or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        prof = json.load(f)
+    cal = prof["calibration"]
+    fs = cal["copy_bytes"] / (cal["FETCH_SIZE_KiB"] * 1024.0)
+    ws = cal["copy_bytes"] / (cal["WRITE_SIZE_KiB"] * 1024.0)
+    names = prof["entry_points"].get(entry.split(":")[0])
+    if not names or any(n not in prof["kernels"] for n in names):
+        return None
+    ks = [prof["kernels"][n] for n in names]
+    return round(sum((k["FETCH_SIZE_KiB"] * fs + k["WRITE_SIZE_KiB"] * ws) * 1024.0 for k in ks))
+
+
 def cpu_baseline(cfg, data, n_tokens):
     """Reference algorithm on host cores: the oracle's torch-CPU restatement of
     models/moe.py, bf16, forward + backward, on the first n_tokens tokens."""
@@ -214,14 +234,15 @@ def main():
     dk = kernels[dom]
     bound, work = model[dom]
     avg_s = dk["avg_us"] / 1e6
+    traffic = hbm_traffic(cfg.name, dom)
     if bound == "mfma":
         roofline = {"kernel": dom, "bound": "mfma", "achieved": round(work / avg_s / 1e12, 2),
                     "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s", "frac": round(work / avg_s / PEAK_BF16_FLOPS, 4),
-                    "traffic": None, "work_per_launch": work}
+                    "traffic": traffic, "work_per_launch": work}
     else:
         roofline = {"kernel": dom, "bound": "hbm", "achieved": round(work / avg_s / 1e9, 1),
                     "peak": PEAK_HBM_BYTES / 1e9, "unit": "GB/s", "frac": round(work / avg_s / PEAK_HBM_BYTES, 4),
-                    "traffic": None, "work_per_launch": work}
+                    "traffic": traffic, "work_per_launch": work}
     gemm_s = sum(kernels[n]["avg_us"] * kernels[n]["calls"] for n in kernels if model.get(n, ("",))[0] == "mfma")
     gemm_s = gemm_s / 1e6 / args.steps
     gemm_flops = cfg.flops_fwd_bwd() / (3.0 if args.fwd_only else 1.0)
