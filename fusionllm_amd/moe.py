@@ -78,7 +78,8 @@ class _MoEBlockFunction(torch.autograd.Function):
     Inputs: (meta, x[T,d], gate.weight, gate.bias, *weights) where weights
     are, per routed expert, (w1, w3, w2) and then the shared expert's
     (w1, w3, w2) when it exists.  Outputs: y[T,d], indices[T,k] int64,
-    weights[T,k] fp32 (the last two are not differentiable).
+    weights[T,k] fp32, expert counts[E] int32 (the last three are not
+    differentiable).
     """
 
     @staticmethod
@@ -101,14 +102,14 @@ class _MoEBlockFunction(torch.autograd.Function):
         ctx.param_dtypes = (gate_w.dtype, gate_b.dtype, [w.dtype for w in weights])
         ctx.x_dtype = x.dtype
         ctx.save_for_backward(xb, gwb, idx, w, v, offsets, perm, pos, x_perm, ab, h, o, *wb)
-        ctx.mark_non_differentiable(idx64, w)
-        # The index and weight outputs never carry gradients: do not let
-        # autograd fill zero tensors for them.
+        ctx.mark_non_differentiable(idx64, w, counts)
+        # The index, weight and count outputs never carry gradients: do not
+        # let autograd fill zero tensors for them.
         ctx.set_materialize_grads(False)
-        return y, idx64, w
+        return y, idx64, w, counts
 
     @staticmethod
-    def backward(ctx, dy, _d_idx, _d_w):
+    def backward(ctx, dy, _d_idx, _d_w, _d_counts):
         E, k, inter, rs, has_shared, out_dtype = ctx.meta
         if dy is None:  # y did not reach the loss
             return (None,) * (4 + len(ctx.param_dtypes[2]))
@@ -176,6 +177,10 @@ class DeepSeekMoE(nn.Module):
         self.shared_expert = SwiGLUExpert(self.dim, self.moe_inter_dim) if self.n_shared_experts > 0 else None
         self._last_indices: torch.Tensor | None = None
         self._last_weights: torch.Tensor | None = None
+        # Per-expert slot counts of the last routing, from the dispatch
+        # kernel's histogram, and the indices tensor they were counted from.
+        self._last_counts: torch.Tensor | None = None
+        self._counts_of: torch.Tensor | None = None
 
     def _flat_weights(self) -> list[torch.Tensor]:
         # Direct dict access: nn.Module.__getattr__ per weight dominates the
@@ -223,13 +228,15 @@ class DeepSeekMoE(nn.Module):
         switch = flat.device.index != torch._C._cuda_getDevice()
         with torch.cuda.device(flat.device) if switch else contextlib.nullcontext():
             if needs_grad:
-                y, idx64, w = _MoEBlockFunction.apply(meta, flat, self.gate.weight, self.gate.bias, *weights)
+                y, idx64, w, counts = _MoEBlockFunction.apply(meta, flat, self.gate.weight, self.gate.bias,
+                                                              *weights)
             else:
                 # inference: the same kernels, nothing kept for a backward pass
                 fw = _forward_pass(meta, flat, self.gate.weight, self.gate.bias, weights)
-                idx64, w, y = fw[4], fw[5], fw[-1]
+                idx64, w, counts, y = fw[4], fw[5], fw[7], fw[-1]
         self._last_indices = idx64
         self._last_weights = w
+        self._last_counts, self._counts_of = counts, idx64
         return y.view(shape)
 
     def _forward_empty(self, flat: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
@@ -239,33 +246,60 @@ class DeepSeekMoE(nn.Module):
         k = self.n_activated_experts
         self._last_indices = torch.empty(0, k, dtype=torch.int64, device=flat.device)
         self._last_weights = torch.empty(0, k, dtype=torch.float32, device=flat.device)
+        self._last_counts = torch.zeros(self.n_routed_experts, dtype=torch.int32, device=flat.device)
+        self._counts_of = self._last_indices
         y = flat.new_zeros(0, self.dim, dtype=out_dtype)
         tied = [self.gate.weight, self.gate.bias]
         if self.shared_expert is not None:
             tied += [self.shared_expert.w1.weight, self.shared_expert.w2.weight, self.shared_expert.w3.weight]
         return y + sum(p.sum() * 0 for p in tied).to(out_dtype) + flat.sum().to(out_dtype) * 0
 
+    def _load(self) -> torch.Tensor:
+        """Slots per expert of the last routing, as the reference's
+        ``bincount(_last_indices, minlength=E).float()`` (models/moe.py:93,105).
+
+        After a forward on the kernels these are the dispatch histogram's
+        counts (no extra pass over the indices).  If ``_last_indices`` was
+        replaced since, they are counted from it as the reference does.
+        """
+        if self._last_counts is not None and self._counts_of is self._last_indices:
+            return self._last_counts.float()
+        return torch.bincount(self._last_indices.flatten(), minlength=self.n_routed_experts).float()
+
     def update_gate_bias(self, speed: float = 0.001) -> None:
-        """Load-balancing bias step from the last routing (reference: models/moe.py:89-98)."""
+        """Load-balancing bias step from the last routing (reference: models/moe.py:89-98).
+
+        Same rule as the reference: experts above 1.10x the mean load lose
+        ``speed`` and experts below 0.90x gain it.  The masked update is
+        written as a select, so it needs no device-to-host synchronisation.
+        """
         if self._last_indices is None:
             return
-        load = torch.bincount(self._last_indices.flatten(), minlength=self.n_routed_experts).float()
+        load = self._load()
         mean = load.mean()
         overloaded = load > mean * 1.10
         underloaded = load < mean * 0.90
         with torch.no_grad():
-            self.gate.bias[overloaded] -= speed
-            self.gate.bias[underloaded] += speed
+            b = self.gate.bias
+            b.copy_(torch.where(overloaded, b - speed, torch.where(underloaded, b + speed, b)))
 
     def get_load_balance_loss(self) -> torch.Tensor:
-        """Diagnostic load-balance loss from the last routing (reference: models/moe.py:100-109)."""
+        """Diagnostic load-balance loss from the last routing (reference: models/moe.py:100-109).
+
+        ``E * sum_e f_e * P_e`` with ``f`` the slot fraction per expert and
+        ``P`` the mean routing weight per expert.  The per-token weight rows
+        are scattered into a [T, E] matrix, which equals the reference's
+        one-hot product summed over the k slots (the k experts of a token are
+        distinct, so each entry is one weight plus zeros), and averaged with
+        the same reduction.
+        """
         if self._last_indices is None or self._last_weights is None:
             return torch.tensor(0.0, device=self.gate.weight.device)
         T, k = self._last_weights.shape
         E = self.n_routed_experts
-        flat_idx = self._last_indices.flatten()
-        load = torch.bincount(flat_idx, minlength=E).float()
+        load = self._load()
         frac = load / (load.sum() + 1e-10)
-        onehot = F.one_hot(flat_idx, num_classes=E).float()
-        prob = (onehot * self._last_weights.flatten().unsqueeze(-1)).view(T, k, E).sum(dim=1).mean(dim=0)
+        w = self._last_weights.float()
+        prob = torch.zeros(T, E, dtype=w.dtype, device=w.device).scatter_add_(
+            1, self._last_indices.reshape(T, k), w.reshape(T, k)).mean(dim=0)
         return (frac * prob).sum() * E

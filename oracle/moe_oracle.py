@@ -12,6 +12,8 @@ Every function follows the reference op by op, in the reference's dtypes:
                                  .to(x.dtype)
   moe_forward     moe.py:79-87   view, route, routed + shared, view back
   block_forward   fusionllm.py:50-53 (ffn half) x + moe(RMSNorm(x)), eps 1e-6
+  gate_bias_step  moe.py:89-98   bincount, 1.10/0.90 x mean thresholds, masked +-speed
+  load_balance_loss moe.py:100-109 E * sum(f * P) with one-hot P
 Router modes:
   "module" — the reference exactly: logits and scores in the module dtype,
              torch.topk (its own tie order);
@@ -133,6 +135,27 @@ def block_forward(x, norm_w, moe_args: dict):
     """FFN half of FusionLLMBlock.forward, models/fusionllm.py:52."""
     y, _, _ = moe_forward(rms_norm(x, norm_w), **moe_args)
     return x + y
+
+
+def gate_bias_step(bias, indices, n_experts: int, speed: float = 0.001):
+    """DeepSeekMoE.update_gate_bias, models/moe.py:89-98; returns the new bias."""
+    b = bias.detach().clone()
+    load = torch.bincount(indices.flatten(), minlength=n_experts).float()
+    mean = load.mean()
+    b[load > mean * 1.10] -= speed
+    b[load < mean * 0.90] += speed
+    return b
+
+
+def load_balance_loss(indices, weights, n_experts: int):
+    """DeepSeekMoE.get_load_balance_loss, models/moe.py:100-109."""
+    T, k = weights.shape
+    flat = indices.flatten()
+    load = torch.bincount(flat, minlength=n_experts).float()
+    frac = load / (load.sum() + 1e-10)
+    onehot = F.one_hot(flat, num_classes=n_experts).float()
+    prob = (onehot * weights.flatten().unsqueeze(-1)).view(T, k, n_experts).sum(dim=1).mean(dim=0)
+    return (frac * prob).sum() * n_experts
 
 
 # ---- C restatement wrappers -------------------------------------------------------

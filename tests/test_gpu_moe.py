@@ -240,19 +240,25 @@ def test_checkpoint_recompute_matches(gpu_device):
             assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
-def test_bias_update_and_aux_loss_on_gpu(gpu_device):
-    cfg = configs.C2
-    data = configs.make_block(cfg, seed=0, tokens=4096)
+@pytest.mark.parametrize("cfg,tokens", [(configs.C2, 4096), (configs.C5, 2048)], ids=["C2", "C5"])
+@pytest.mark.parametrize("train", [False, True], ids=["inference", "training"])
+def test_bias_update_and_aux_loss_on_gpu(gpu_device, cfg, tokens, train):
+    # The dispatch histogram stands in for bincount (models/moe.py:93,105):
+    # the counts, the bias step and the loss equal the reference formulas.
+    data = configs.make_block(cfg, seed=0, tokens=tokens)
     m = build_module(cfg, data, gpu_device)
-    with torch.no_grad():
-        m(data.x.to(gpu_device, torch.bfloat16))
-    before = m.gate.bias.detach().clone()
-    m.update_gate_bias(0.001)
-    counts = torch.bincount(m._last_indices.flatten(), minlength=8).float()
-    over, under = counts > counts.mean() * 1.1, counts < counts.mean() * 0.9
-    want = before.clone()
-    want[over] -= 0.001
-    want[under] += 0.001
-    assert torch.equal(m.gate.bias.detach(), want)
+    x = data.x.to(gpu_device, torch.bfloat16)
+    with torch.set_grad_enabled(train):
+        y = m(x.requires_grad_(train))
+    if train:
+        y.float().sum().backward()
+    E = cfg.n_experts
+    idx, w = m._last_indices, m._last_weights
+    assert m._counts_of is idx
+    assert torch.equal(m._last_counts.long(), torch.bincount(idx.flatten(), minlength=E))
+    want_loss = mo.load_balance_loss(idx, w, E)
     loss = m.get_load_balance_loss()
-    assert loss.requires_grad is False and torch.isfinite(loss)
+    assert loss.requires_grad is False and torch.equal(loss, want_loss)
+    want_bias = mo.gate_bias_step(m.gate.bias, idx, E, 0.001)
+    m.update_gate_bias(0.001)
+    assert torch.equal(m.gate.bias.detach(), want_bias)

@@ -122,6 +122,36 @@ def test_update_gate_bias_and_aux_loss_semantics():
     assert torch.allclose(m.get_load_balance_loss(), (f * P).sum() * 8)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_aux_outputs_match_reference_formulas_bitwise(dtype):
+    # Both count sources (dispatch counts recorded at forward, or bincount of
+    # a replaced _last_indices) against models/moe.py:89-109 as written.
+    from oracle import moe_oracle as mo
+    g = torch.Generator().manual_seed(3)
+    for E, k, T in ((8, 2, 257), (64, 6, 300)):
+        cfg = dict(configs.C2.moe_config(), n_routed_experts=E, n_activated_experts=k)
+        m = DeepSeekMoE(cfg).to(dtype)
+        with torch.no_grad():
+            m.gate.bias.uniform_(-0.1, 0.1, generator=g)
+        idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)])
+        for t in range(T // 2):  # skew: half the tokens pick expert 0 first
+            r = idx[t].tolist()
+            r.remove(0) if 0 in r else r.pop()
+            idx[t] = torch.tensor([0] + r)
+        w = torch.rand(T, k, generator=g)
+        w = w / w.sum(-1, keepdim=True)
+        for recorded in (False, True):
+            m._last_indices, m._last_weights = idx, w
+            if recorded:
+                m._last_counts = torch.bincount(idx.flatten(), minlength=E).int()
+                m._counts_of = idx
+            want = mo.gate_bias_step(m.gate.bias, idx, E, 0.003)
+            loss = m.get_load_balance_loss()
+            assert torch.equal(loss, mo.load_balance_loss(idx, w, E))
+            m.update_gate_bias(0.003)
+            assert torch.equal(m.gate.bias.detach(), want)
+
+
 def test_swiglu_expert_forward_matches_closed_form():
     e = SwiGLUExpert(16, 32).double()
     x = torch.randn(5, 16, dtype=torch.float64)
