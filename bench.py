@@ -40,7 +40,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--config", default="C2-bf16-fwdbwd-skewed")
+    p.add_argument("--config", default="C2-bf16-fwdbwd-skewed",
+                   help="workload name from fusionllm_amd.configs, or its prefix C1..C5")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-tokens", type=int, default=2048, help="token sample for the CPU baseline")
     p.add_argument("--fwd-only", action="store_true",
@@ -85,6 +86,10 @@ def kernel_model(cfg, T):
         "combine_bwd": ("hbm", T * k * (2 * d + 2 * d + 2 * d + 4 + 4 + 4)),
         "router_bwd": ("hbm", T * k * (2 * d + 4 * 4)),
         "dx_reduce": ("hbm", T * (k * 2 * d + 2 * d + 2 * d + 12 * k)),
+        # C4 (RMSNorm + MoE + residual): x in, xn and rstd out; the backward
+        # reads the k routed + shared rows, x and d_out and writes dx
+        "rmsnorm_fwd": ("hbm", T * (2 * d + 2 * d + 4)),
+        "dx_reduce_norm": ("hbm", T * (k * 2 * d + 2 * d + 2 * d + 2 * d + 2 * d + 12 * k + 4)),
         "transpose_weights": ("hbm", (E + (1 if cfg.n_shared else 0)) * 3 * d * I * 2 * 2),
     }
 
@@ -123,12 +128,20 @@ def cpu_baseline(cfg, data, n_tokens):
     x0 = data.x[:T].bfloat16()
     dy = data.dy[:T].bfloat16()
 
+    norm_w = torch.ones(cfg.dim, dtype=torch.bfloat16, requires_grad=True)
+
     def step():
         for t in sd.values():
             t.grad = None
         x = x0.clone().requires_grad_(True)
-        y, _, _ = mo.moe_forward(x, sd["gate.weight"], sd["gate.bias"], experts, shared, cfg.topk,
-                                 cfg.route_scale, mode="module")
+        if cfg.layers == 1:
+            y, _, _ = mo.moe_forward(x, sd["gate.weight"], sd["gate.bias"], experts, shared, cfg.topk,
+                                     cfg.route_scale, mode="module")
+        else:  # the stack: the same block weights in every layer (time, not values, is measured)
+            y = x
+            for _ in range(cfg.layers):
+                y = y + mo.moe_forward(mo.rms_norm(y, norm_w), sd["gate.weight"], sd["gate.bias"], experts,
+                                       shared, cfg.topk, cfg.route_scale, mode="module")[0]
         y.backward(dy)
 
     step()  # warmup
@@ -146,8 +159,10 @@ def cpu_baseline(cfg, data, n_tokens):
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"{cfg.name}: first {T} of {cfg.tokens} tokens, reference module semantics (bf16 router), "
-                   f"bf16 forward+backward in torch CPU, median of {len(times)} after 1 warmup"),
+        "sample": (f"{cfg.name}: first {T} of {cfg.tokens} tokens"
+                   + (f", {cfg.layers} x (RMSNorm + MoE + residual)" if cfg.layers > 1 else "")
+                   + f", reference module semantics (bf16 router), bf16 forward+backward in torch CPU, "
+                   f"median of {len(times)} after 1 warmup"),
     }
 
 
@@ -160,29 +175,51 @@ def main():
         print(json.dumps({"error": "this build measures one GPU only (one MI355X per box); "
                                    "run without --gpus or with --gpus 1"}))
         sys.exit(2)
-    from fusionllm_amd import DeepSeekMoE, configs
+    from fusionllm_amd import DeepSeekMoE, configs, moe_residual
     from fusionllm_amd import _kernels as K
 
-    cfg = configs.ALL[args.config]
+    cfg = configs.ALL.get(args.config) or next(
+        (c for n, c in configs.ALL.items() if n.split("-")[0] == args.config), None)
+    if cfg is None:
+        raise SystemExit(f"unknown --config {args.config!r}: one of {sorted(configs.ALL)} or C1..C5")
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     data = configs.make_block(cfg, seed=0)
-    m = DeepSeekMoE(cfg.moe_config())
-    m.load_state_dict({k: v.bfloat16() for k, v in data.state_dict().items()})
-    m = m.to(device=dev, dtype=torch.bfloat16)
+
+    def module(d):
+        m = DeepSeekMoE(cfg.moe_config())
+        m.load_state_dict({k: v.bfloat16() for k, v in d.state_dict().items()})
+        return m.to(device=dev, dtype=torch.bfloat16)
+
+    # C4: a stack of cfg.layers blocks x + MoE(RMSNorm(x)) (models/fusionllm.py:48,52),
+    # independent seeded weights per layer, norm weights ones (their init).
+    mods = [module(data)] + [module(configs.make_block(cfg, seed=l, with_dy=False))
+                             for l in range(1, cfg.layers)]
+    norms = [torch.nn.RMSNorm(cfg.dim, eps=1e-6).to(device=dev, dtype=torch.bfloat16)
+             for _ in range(cfg.layers)] if cfg.layers > 1 else []
     x = data.x.to(dev, torch.bfloat16).requires_grad_(True)
     dy = data.dy.to(dev, torch.bfloat16)
     T = x.shape[0]
 
+    def forward():
+        if not norms:
+            return mods[0](x)
+        h = x
+        for m, n in zip(mods, norms):
+            h = moe_residual(h, n, m)
+        return h
+
     def step():
         if args.fwd_only:
             with torch.no_grad():
-                m(x)
+                forward()
             return
-        m.zero_grad(set_to_none=True)
+        for m in mods:
+            m.zero_grad(set_to_none=True)
+        for n in norms:
+            n.weight.grad = None
         x.grad = None
-        y = m(x)
-        y.backward(dy)
+        forward().backward(dy)
 
     for _ in range(args.warmup):
         step()
@@ -252,7 +289,9 @@ def main():
         cpu = cpu_baseline(cfg, data, args.cpu_tokens)
 
     line = {
-        "metric": METRIC if not args.fwd_only else "MoE block forward tokens/sec (bf16)",
+        "metric": (METRIC if cfg.layers == 1 else
+                   f"MoE FFN stack ({cfg.layers} x RMSNorm+MoE+residual) tokens/sec fwd+bwd (bf16)")
+        if not args.fwd_only else "MoE block forward tokens/sec (bf16)",
         "value": round(tok_s, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -266,7 +305,8 @@ def main():
         "data": f"synthetic (seeded N(0,1) input, N(0,0.02^2) weights, router bias {cfg.bias})",
         "config": {"workload": cfg.name, "tokens": T, "dim": cfg.dim, "inter": cfg.inter,
                    "experts": cfg.n_experts, "topk": cfg.topk, "shared": int(cfg.n_shared > 0),
-                   "bias": cfg.bias, "pass": "forward" if args.fwd_only else "forward+backward"},
+                   "bias": cfg.bias, "layers": cfg.layers,
+                   "pass": "forward" if args.fwd_only else "forward+backward"},
         "grouped_gemm_mfma_frac": round(gemm_flops / gemm_s / PEAK_BF16_FLOPS, 4),
         "step_mfma_frac": round(gemm_flops / (elapsed / args.steps) / PEAK_BF16_FLOPS, 4),
         "roofline": roofline,

@@ -3,8 +3,9 @@
 Drop-in replacement for ``models.moe`` of FusionLLM: ``DeepSeekMoE`` and
 ``SwiGLUExpert`` with the reference's constructor, parameters and methods,
 computed by hand-written gfx950 HIP kernels (libfusionmoe.so, C ABI in
-include/fusionmoe.h).
+include/fusionmoe.h); ``moe_residual`` runs FusionLLMBlock's FFN half
+x + ffn(norm2(x)) with the RMSNorm and the residual fused into the kernels.
 """
-from .moe import DeepSeekMoE, SwiGLUExpert
+from .moe import DeepSeekMoE, SwiGLUExpert, moe_residual
 
-__all__ = ["DeepSeekMoE", "SwiGLUExpert"]
+__all__ = ["DeepSeekMoE", "SwiGLUExpert", "moe_residual"]

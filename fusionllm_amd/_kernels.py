@@ -147,15 +147,17 @@ def down_fwd(h, offsets, n_experts: int, rows_routed: int, rows_shared: int, w2s
 
 
 @_timed
-def combine_fwd(expert_out, idx, weights, pos, rows_routed: int, has_shared: bool, out_dtype: torch.dtype):
+def combine_fwd(expert_out, idx, weights, pos, rows_routed: int, has_shared: bool, out_dtype: torch.dtype,
+                residual: torch.Tensor | None = None):
     lib = _lib.load()
     T, k = idx.shape
     d = expert_out.shape[1]
     y = torch.empty(T, d, dtype=out_dtype, device=expert_out.device)
+    res = 0 if residual is None else _req(residual, "residual", out_dtype)
     check(lib.fmoe_combine_fwd(_req(expert_out, "expert_out", torch.bfloat16), _req(idx, "idx", torch.int32),
                                _req(weights, "weights", torch.float32), _req(pos, "pos_of_slot", torch.int32),
-                               T, d, k, rows_routed, int(has_shared), _dtype_code(out_dtype), y.data_ptr(),
-                               _stream()),
+                               T, d, k, rows_routed, int(has_shared), _dtype_code(out_dtype), res,
+                               y.data_ptr(), _stream()),
           "fmoe_combine_fwd")
     return y
 
@@ -284,3 +286,45 @@ def dx_reduce(dx_rows, pos, idx, d_logits, gate_w, rows_routed: int, has_shared:
                              _dtype_code(out_dtype), dx.data_ptr(), _stream()),
           "fmoe_dx_reduce")
     return dx
+
+
+@_timed
+def rmsnorm_fwd(x, norm_w, eps: float):
+    """RMSNorm of the rows of x into the bf16 MoE input; returns (xn, rstd)."""
+    lib = _lib.load()
+    T, d = x.shape
+    xn = torch.empty(T, d, dtype=torch.bfloat16, device=x.device)
+    rstd = torch.empty(T, dtype=torch.float32, device=x.device)
+    w_ptr = 0 if norm_w is None else _req(norm_w, "norm weight")
+    w_code = F32 if norm_w is None else _dtype_code(norm_w.dtype)
+    check(lib.fmoe_rmsnorm_fwd(_req(x, "x"), _dtype_code(x.dtype), w_ptr, w_code, T, d, float(eps),
+                               xn.data_ptr(), rstd.data_ptr(), _stream()),
+          "fmoe_rmsnorm_fwd")
+    return xn, rstd
+
+
+@_timed
+def dx_reduce_norm(dx_rows, pos, idx, d_logits, gate_w, rows_routed: int, has_shared: bool,
+                   x, rstd, norm_w, d_out, want_dw: bool):
+    """Input gradient of x + moe(rmsnorm(x)) and the norm weight's gradient."""
+    lib = _lib.load()
+    T, k = idx.shape
+    d = dx_rows.shape[1]
+    dev = dx_rows.device
+    dx = torch.empty(T, d, dtype=x.dtype, device=dev)
+    dnw, ws, ws_bytes = None, None, 0
+    if want_dw and norm_w is not None:
+        dnw = torch.empty(d, dtype=norm_w.dtype, device=dev)
+        ws_bytes = lib.fmoe_norm_bwd_workspace_bytes(d)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    w_ptr = 0 if norm_w is None else _req(norm_w, "norm weight")
+    w_code = F32 if norm_w is None else _dtype_code(norm_w.dtype)
+    check(lib.fmoe_dx_reduce_norm(_req(dx_rows, "dx_rows", torch.bfloat16), _req(pos, "pos_of_slot", torch.int32),
+                                  _req(idx, "idx", torch.int32), _req(d_logits, "d_logits", torch.float32),
+                                  _req(gate_w, "gate.weight", torch.bfloat16), T, d, k, rows_routed,
+                                  int(has_shared), _req(x, "x"), _req(rstd, "rstd", torch.float32), w_ptr,
+                                  w_code, _req(d_out, "d_out", x.dtype), _dtype_code(x.dtype), dx.data_ptr(),
+                                  0 if dnw is None else dnw.data_ptr(), 0 if ws is None else ws.data_ptr(),
+                                  ws_bytes, _stream()),
+          "fmoe_dx_reduce_norm")
+    return dx, dnw

@@ -13,7 +13,7 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_size_t, c_void_
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libfusionmoe.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 MAX_EXPERTS = 64
 MAX_TOPK = 8
 
@@ -39,7 +39,7 @@ SIGNATURES = {
     "fmoe_down_fwd": (c_int, [_P, _P, c_int, c_int64, c_int64, c_int64, c_int64,
                               _PP, _P, _P, c_size_t, _P]),
     "fmoe_combine_fwd": (c_int, [_P, _P, _P, _P, c_int64, c_int64, c_int, c_int64,
-                                 c_int, c_int, _P, _P]),
+                                 c_int, c_int, _P, _P, _P]),
     "fmoe_combine_bwd": (c_int, [_P, c_int, _P, _P, _P, c_int64, c_int64, c_int,
                                  _P, _P, _P]),
     "fmoe_transpose_weights": (c_int, [_PP, _PP, _PP, c_int, c_int64, c_int64, _P, _P, _P]),
@@ -56,6 +56,10 @@ SIGNATURES = {
                                 _P, _P, _P, c_int, _P, c_size_t, _P]),
     "fmoe_dx_reduce": (c_int, [_P, _P, _P, _P, _P, c_int64, c_int64, c_int, c_int64,
                                c_int, c_int, _P, _P]),
+    "fmoe_rmsnorm_fwd": (c_int, [_P, c_int, _P, c_int, c_int64, c_int64, c_float, _P, _P, _P]),
+    "fmoe_norm_bwd_workspace_bytes": (c_size_t, [c_int64]),
+    "fmoe_dx_reduce_norm": (c_int, [_P, _P, _P, _P, _P, c_int64, c_int64, c_int, c_int64, c_int,
+                                    _P, _P, _P, c_int, _P, c_int, _P, _P, _P, c_size_t, _P]),
 }
 
 _lock = threading.Lock()

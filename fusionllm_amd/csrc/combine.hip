@@ -8,56 +8,16 @@
 // and adds them in ascending expert index, each product rounded to fp32
 // before the add, which is the reference's rounding sequence.
 #include "fmoe_common.h"
+#include "choices.h"
 
 namespace fmoe {
-
-// Load the k choices of token t and return them in ascending expert order
-// (the experts of one token are distinct).
-struct Choices {
-  int e[FMOE_MAX_TOPK];
-  int pos[FMOE_MAX_TOPK];
-  float w[FMOE_MAX_TOPK];
-  int slot[FMOE_MAX_TOPK];
-};
-
-__device__ __forceinline__ void load_sorted_choices(const int32_t* idx, const int32_t* pos_of_slot,
-                                                    const float* weights, int64_t t, int k,
-                                                    Choices& c) {
-#pragma unroll
-  for (int j = 0; j < FMOE_MAX_TOPK; ++j) {
-    if (j < k) {
-      const int64_t s = t * k + j;
-      c.e[j] = idx[s];
-      c.pos[j] = pos_of_slot[s];
-      c.w[j] = weights ? weights[s] : 0.0f;
-      c.slot[j] = j;
-    } else {
-      c.e[j] = 0x7fffffff;
-      c.pos[j] = 0;
-      c.w[j] = 0.0f;
-      c.slot[j] = j;
-    }
-  }
-  // Odd-even transposition sort on 8 entries (padding sorts to the end).
-#pragma unroll
-  for (int pass = 0; pass < FMOE_MAX_TOPK; ++pass) {
-#pragma unroll
-    for (int j = pass & 1; j + 1 < FMOE_MAX_TOPK; j += 2) {
-      if (c.e[j] > c.e[j + 1]) {
-        int te = c.e[j]; c.e[j] = c.e[j + 1]; c.e[j + 1] = te;
-        int tp = c.pos[j]; c.pos[j] = c.pos[j + 1]; c.pos[j + 1] = tp;
-        float tw = c.w[j]; c.w[j] = c.w[j + 1]; c.w[j + 1] = tw;
-        int ts = c.slot[j]; c.slot[j] = c.slot[j + 1]; c.slot[j + 1] = ts;
-      }
-    }
-  }
-}
 
 // One thread per (token, 8-column chunk).
 __global__ __launch_bounds__(256) void combine_fwd_kernel(
     const uint16_t* __restrict__ eo, const int32_t* __restrict__ idx,
     const float* __restrict__ weights, const int32_t* __restrict__ pos_of_slot, int64_t T,
-    int dim, int k, int64_t rows_routed, int has_shared, int out_dtype, void* __restrict__ y) {
+    int dim, int k, int64_t rows_routed, int has_shared, int out_dtype,
+    const void* __restrict__ residual, void* __restrict__ y) {
   const int chunks = dim / 8;
   const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (g >= T * chunks) return;
@@ -81,13 +41,28 @@ __global__ __launch_bounds__(256) void combine_fwd_kernel(
     float r[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) r[i] = bf_round(acc[i]) + sh[i];
+    if (residual) {
+      // x + moe(x'): the block output rounded to bf16, then the bf16 add.
+      float xr[8];
+      unpack8(reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(residual) + t * dim)[c], xr);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r[i] = xr[i] + bf_round(r[i]);
+    }
     reinterpret_cast<uint4*>(static_cast<uint16_t*>(y) + t * dim)[c] = pack8(r);
   } else {
+    float r[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = acc[i] + sh[i];
+    if (residual) {
+      const float4* xp = reinterpret_cast<const float4*>(static_cast<const float*>(residual) + t * dim + c * 8);
+      const float4 a = xp[0], b = xp[1];
+      const float xr[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r[i] = xr[i] + r[i];
+    }
     float* yo = static_cast<float*>(y) + t * dim + c * 8;
-    float4 v0 = make_float4(acc[0] + sh[0], acc[1] + sh[1], acc[2] + sh[2], acc[3] + sh[3]);
-    float4 v1 = make_float4(acc[4] + sh[4], acc[5] + sh[5], acc[6] + sh[6], acc[7] + sh[7]);
-    reinterpret_cast<float4*>(yo)[0] = v0;
-    reinterpret_cast<float4*>(yo)[1] = v1;
+    reinterpret_cast<float4*>(yo)[0] = make_float4(r[0], r[1], r[2], r[3]);
+    reinterpret_cast<float4*>(yo)[1] = make_float4(r[4], r[5], r[6], r[7]);
   }
 }
 
@@ -182,18 +157,19 @@ using namespace fmoe;
 
 extern "C" int fmoe_combine_fwd(const void* expert_out, const int32_t* idx, const float* weights,
                                 const int32_t* pos_of_slot, int64_t T, int64_t dim, int k,
-                                int64_t rows_routed, int has_shared, int out_dtype, void* y,
-                                void* stream) {
+                                int64_t rows_routed, int has_shared, int out_dtype,
+                                const void* residual, void* y, void* stream) {
   if (T < 0 || dim <= 0 || rows_routed < 0) return FMOE_ERR_INVALID_ARG;
   if (k <= 0 || k > FMOE_MAX_TOPK || dim % 64 != 0) return FMOE_ERR_SHAPE;
   if (out_dtype != FMOE_BF16 && out_dtype != FMOE_F32) return FMOE_ERR_DTYPE;
   if (T == 0) return FMOE_OK;
   if (!expert_out || !idx || !weights || !pos_of_slot || !y) return FMOE_ERR_INVALID_ARG;
-  if (!aligned16(expert_out) || !aligned16(y)) return FMOE_ERR_ALIGN;
+  if (!aligned16(expert_out) || !aligned16(y) || (residual && !aligned16(residual)))
+    return FMOE_ERR_ALIGN;
   const int64_t total = T * (dim / 8);
   combine_fwd_kernel<<<dim3(ceil_div(total, 256)), dim3(256), 0, as_stream(stream)>>>(
       static_cast<const uint16_t*>(expert_out), idx, weights, pos_of_slot, T, (int)dim, k,
-      rows_routed, has_shared, out_dtype, y);
+      rows_routed, has_shared, out_dtype, residual, y);
   return launch_status();
 }
 

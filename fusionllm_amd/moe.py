@@ -52,9 +52,10 @@ def _as_bf16(t: torch.Tensor) -> torch.Tensor:
     return t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)
 
 
-def _forward_pass(meta, x, gate_w, gate_b, weights):
+def _forward_pass(meta, x, gate_w, gate_b, weights, residual=None):
     """The forward kernels of DeepSeekMoE.forward (models/moe.py:79-87); returns
-    the output and every intermediate the backward pass needs."""
+    the output and every intermediate the backward pass needs.  With a
+    residual the output is residual + moe(x) (models/fusionllm.py:52)."""
     E, k, inter, rs, has_shared, out_dtype = meta
     T, d = x.shape
     xb = _as_bf16(x).contiguous()
@@ -68,8 +69,76 @@ def _forward_pass(meta, x, gate_w, gate_b, weights):
     rows_r, rows_s = T * k, (T if has_shared else 0)
     ab, h = K.gateup_fwd(x_perm, xb if has_shared else None, offsets, E, w1s, w3s, inter)
     o = K.down_fwd(h, offsets, E, rows_r, rows_s, w2s, d)
-    y = K.combine_fwd(o, idx, w, pos, rows_r, has_shared, out_dtype)
+    y = K.combine_fwd(o, idx, w, pos, rows_r, has_shared, out_dtype, residual)
     return xb, gwb, wb, idx, idx64, w, v, counts, offsets, perm, pos, x_perm, ab, h, o, y
+
+
+def _save_forward(ctx, meta, fw, gate_w, gate_b, weights):
+    """Keep what the backward kernels read; the expert counts travel to the
+    host asynchronously and are read at the end of backward.  Returns the
+    tensors to save."""
+    E = meta[0]
+    xb, gwb, wb, idx, idx64, w, v, counts, offsets, perm, pos, x_perm, ab, h, o, y = fw
+    # Experts that get no tokens return None gradients (the reference never
+    # puts them in the graph, moe.py:66-72).
+    counts_host = torch.empty(E, dtype=torch.int32, pin_memory=True)
+    counts_host.copy_(counts, non_blocking=True)
+    ev = torch.cuda.Event()
+    ev.record()
+    ctx.meta = meta
+    ctx.counts_host = counts_host
+    ctx.counts_event = ev
+    ctx.param_dtypes = (gate_w.dtype, gate_b.dtype, [t.dtype for t in weights])
+    ctx.mark_non_differentiable(idx64, w, counts)
+    # The index, weight and count outputs never carry gradients: do not let
+    # autograd fill zero tensors for them.
+    ctx.set_materialize_grads(False)
+    return (xb, gwb, idx, w, v, offsets, perm, pos, x_perm, ab, h, o, *wb)
+
+
+def _backward_pass(ctx, saved, dy):
+    """Backward kernels of the MoE (autograd of models/moe.py:44-87) up to,
+    not including, the per-token input-gradient reduction.  Returns
+    (dx_rows, d_logits, dgw, dgb, grads_w) with grads_w per weight, None
+    for experts that got no tokens."""
+    E, k, inter, rs, has_shared, out_dtype = ctx.meta
+    xb, gwb, idx, w, v, offsets, perm, pos, x_perm, ab, h, o, *wb = saved
+    T, d = xb.shape
+    G = E + (1 if has_shared else 0)
+    w1s, w3s, w2s = wb[0::3][:G], wb[1::3][:G], wb[2::3][:G]
+    rows_r, rows_s = T * k, (T if has_shared else 0)
+    gw_dtype, gb_dtype, w_dtypes = ctx.param_dtypes
+
+    # Combine backward: routed rows get dy*w (bf16), slots get <dy, o>.
+    d_o, d_w = K.combine_bwd(dy, o, w, perm, k)
+    dy_sh = _as_bf16(dy).contiguous() if has_shared else None
+
+    # Transposed weight copies for the dX products (one launch for all groups).
+    w13t, w2t = K.transpose_weights(w1s, w3s, w2s)
+    # Down projection: dX with the SwiGLU backward fused, then dW2.
+    d_ab = K.down_bwd_dx(d_o, dy_sh, offsets, E, w2t, ab, inter)
+    dw2 = [torch.empty(d, inter, dtype=w_dtypes[3 * g + 2], device=xb.device) for g in range(G)]
+    K.weight_grad(d_o, dy_sh, h, None, offsets, E, rows_r, rows_s, d, dw2, None,
+                  w_dtypes[2], tag="w2")
+    # Gate/up projections: dX (one product over [w1; w3]) then dW1, dW3.
+    dx_rows = K.gateup_bwd_dx(d_ab, offsets, E, rows_r, rows_s, w13t, d)
+    dw1 = [torch.empty(inter, d, dtype=w_dtypes[3 * g], device=xb.device) for g in range(G)]
+    dw3 = [torch.empty(inter, d, dtype=w_dtypes[3 * g + 1], device=xb.device) for g in range(G)]
+    K.weight_grad(d_ab, None, x_perm, xb if has_shared else None, offsets, E, rows_r, rows_s,
+                  inter, dw1, dw3, w_dtypes[0], tag="w13")
+    # Router: logits gradient, gate weight/bias gradient.
+    d_logits, dgw, dgb = K.router_bwd(d_w, v, perm, offsets, x_perm, E, rs, gw_dtype)
+    if dgb.dtype != gb_dtype:
+        dgb = dgb.to(gb_dtype)
+
+    ctx.counts_event.synchronize()
+    counts = ctx.counts_host.tolist()
+    grads_w = [None] * len(wb)
+    for g in range(G):
+        if g < E and counts[g] == 0:
+            continue
+        grads_w[3 * g], grads_w[3 * g + 1], grads_w[3 * g + 2] = dw1[g], dw3[g], dw2[g]
+    return dx_rows, d_logits, dgw, dgb, grads_w
 
 
 class _MoEBlockFunction(torch.autograd.Function):
@@ -84,76 +153,64 @@ class _MoEBlockFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, meta, x, gate_w, gate_b, *weights):
-        E, k, inter, rs, has_shared, out_dtype = meta
         fw = _forward_pass(meta, x, gate_w, gate_b, weights)
-        xb, gwb, wb, idx, idx64, w, v, counts, offsets, perm, pos, x_perm, ab, h, o, y = fw
-
-        # Experts that get no tokens return None gradients (the reference never
-        # puts them in the graph, moe.py:66-72).  Their counts travel to the
-        # host asynchronously and are read at the end of backward.
-        counts_host = torch.empty(E, dtype=torch.int32, pin_memory=True)
-        counts_host.copy_(counts, non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record()
-
-        ctx.meta = meta
-        ctx.counts_host = counts_host
-        ctx.counts_event = ev
-        ctx.param_dtypes = (gate_w.dtype, gate_b.dtype, [w.dtype for w in weights])
         ctx.x_dtype = x.dtype
-        ctx.save_for_backward(xb, gwb, idx, w, v, offsets, perm, pos, x_perm, ab, h, o, *wb)
-        ctx.mark_non_differentiable(idx64, w, counts)
-        # The index, weight and count outputs never carry gradients: do not
-        # let autograd fill zero tensors for them.
-        ctx.set_materialize_grads(False)
+        ctx.save_for_backward(*_save_forward(ctx, meta, fw, gate_w, gate_b, weights))
+        idx64, w, counts, y = fw[4], fw[5], fw[7], fw[-1]
         return y, idx64, w, counts
 
     @staticmethod
     def backward(ctx, dy, _d_idx, _d_w, _d_counts):
-        E, k, inter, rs, has_shared, out_dtype = ctx.meta
         if dy is None:  # y did not reach the loss
             return (None,) * (4 + len(ctx.param_dtypes[2]))
-        xb, gwb, idx, w, v, offsets, perm, pos, x_perm, ab, h, o, *wb = ctx.saved_tensors
-        T, d = xb.shape
-        G = E + (1 if has_shared else 0)
-        w1s, w3s, w2s = wb[0::3][:G], wb[1::3][:G], wb[2::3][:G]
-        rows_r, rows_s = T * k, (T if has_shared else 0)
-        gw_dtype, gb_dtype, w_dtypes = ctx.param_dtypes
-
-        dy = dy.contiguous()
-        # Combine backward: routed rows get dy*w (bf16), slots get <dy, o>.
-        d_o, d_w = K.combine_bwd(dy, o, w, perm, k)
-        dy_sh = _as_bf16(dy).contiguous() if has_shared else None
-
-        # Transposed weight copies for the dX products (one launch for all groups).
-        w13t, w2t = K.transpose_weights(w1s, w3s, w2s)
-        # Down projection: dX with the SwiGLU backward fused, then dW2.
-        d_ab = K.down_bwd_dx(d_o, dy_sh, offsets, E, w2t, ab, inter)
-        grads_w = [None] * len(wb)
-        dw2 = [torch.empty(d, inter, dtype=w_dtypes[3 * g + 2], device=xb.device) for g in range(G)]
-        K.weight_grad(d_o, dy_sh, h, None, offsets, E, rows_r, rows_s, d, dw2, None,
-                      w_dtypes[2], tag="w2")
-        # Gate/up projections: dX (one product over [w1; w3]) then dW1, dW3.
-        dx_rows = K.gateup_bwd_dx(d_ab, offsets, E, rows_r, rows_s, w13t, d)
-        dw1 = [torch.empty(inter, d, dtype=w_dtypes[3 * g], device=xb.device) for g in range(G)]
-        dw3 = [torch.empty(inter, d, dtype=w_dtypes[3 * g + 1], device=xb.device) for g in range(G)]
-        K.weight_grad(d_ab, None, x_perm, xb if has_shared else None, offsets, E, rows_r, rows_s,
-                      inter, dw1, dw3, w_dtypes[0], tag="w13")
-        # Router: logits gradient, gate weight/bias gradient.
-        d_logits, dgw, dgb = K.router_bwd(d_w, v, perm, offsets, x_perm, E, rs, gw_dtype)
-        if dgb.dtype != gb_dtype:
-            dgb = dgb.to(gb_dtype)
+        saved = ctx.saved_tensors
+        E, k, inter, rs, has_shared, out_dtype = ctx.meta
+        xb, gwb, idx, pos = saved[0], saved[1], saved[2], saved[7]
+        dx_rows, d_logits, dgw, dgb, grads_w = _backward_pass(ctx, saved, dy.contiguous())
         dx = None
         if ctx.needs_input_grad[1]:
-            dx = K.dx_reduce(dx_rows, pos, idx, d_logits, gwb, rows_r, has_shared, ctx.x_dtype)
-
-        ctx.counts_event.synchronize()
-        counts = ctx.counts_host.tolist()
-        for g in range(G):
-            if g < E and counts[g] == 0:
-                continue
-            grads_w[3 * g], grads_w[3 * g + 1], grads_w[3 * g + 2] = dw1[g], dw3[g], dw2[g]
+            dx = K.dx_reduce(dx_rows, pos, idx, d_logits, gwb, idx.shape[0] * k, has_shared, ctx.x_dtype)
         return (None, dx, dgw, dgb, *grads_w)
+
+
+class _NormMoEResidualFunction(torch.autograd.Function):
+    """x + DeepSeekMoE(RMSNorm(x)), the FFN half of FusionLLMBlock.forward
+    (models/fusionllm.py:48,52), on the kernels: the norm writes the bf16 MoE
+    input, the combine adds the residual, and the backward folds the RMSNorm
+    backward and the residual's gradient into the per-token reduction.
+
+    Inputs: (meta, eps, x[T,d], norm.weight or None, gate.weight, gate.bias,
+    *weights).  Outputs as _MoEBlockFunction.
+    """
+
+    @staticmethod
+    def forward(ctx, meta, eps, x, norm_w, gate_w, gate_b, *weights):
+        xc = x.contiguous()
+        nw = None if norm_w is None else norm_w.contiguous()
+        xn, rstd = K.rmsnorm_fwd(xc, nw, eps)
+        fw = _forward_pass(meta, xn, gate_w, gate_b, weights, residual=xc)
+        saved = _save_forward(ctx, meta, fw, gate_w, gate_b, weights)
+        ctx.has_norm_w = nw is not None
+        ctx.save_for_backward(xc, rstd, nw, *saved)
+        idx64, w, counts, y = fw[4], fw[5], fw[7], fw[-1]
+        return y, idx64, w, counts
+
+    @staticmethod
+    def backward(ctx, dy, _d_idx, _d_w, _d_counts):
+        n_w = len(ctx.param_dtypes[2])
+        if dy is None:
+            return (None,) * (6 + n_w)
+        xc, rstd, nw, *saved = ctx.saved_tensors
+        E, k, inter, rs, has_shared, out_dtype = ctx.meta
+        gwb, idx, pos = saved[1], saved[2], saved[7]
+        dy = dy.contiguous()
+        dx_rows, d_logits, dgw, dgb, grads_w = _backward_pass(ctx, saved, dy)
+        want_dw = ctx.has_norm_w and ctx.needs_input_grad[3]
+        dx, dnw = K.dx_reduce_norm(dx_rows, pos, idx, d_logits, gwb, idx.shape[0] * k, has_shared,
+                                   xc, rstd, nw, dy, want_dw)
+        if not ctx.needs_input_grad[2]:
+            dx = None
+        return (None, None, dx, dnw, dgw, dgb, *grads_w)
 
 
 class DeepSeekMoE(nn.Module):
@@ -217,27 +274,64 @@ class DeepSeekMoE(nn.Module):
             raise RuntimeError("fusionllm_amd.DeepSeekMoE runs on a ROCm device only (got a CPU tensor)")
         weights = self._flat_weights()
         out_dtype = self._output_dtype(flat, weights)
-        E, k = self.n_routed_experts, self.n_activated_experts
         if flat.shape[0] == 0:
             return self._forward_empty(flat, out_dtype).view(shape)
+        return self._run(flat, weights, out_dtype).view(shape)
+
+    def forward_norm_residual(self, x: torch.Tensor, norm: nn.RMSNorm) -> torch.Tensor:
+        """``x + self(norm(x))`` in one pass: the FFN half of
+        FusionLLMBlock.forward (models/fusionllm.py:52) with its
+        ``norm2 = nn.RMSNorm(dim, eps=1e-6)`` (models/fusionllm.py:48).
+
+        The norm's parameters stay in ``norm`` (its weight gets its gradient
+        as usual).  Same dtype rules as ``forward``, with x standing for the
+        norm's output; a bf16 x needs a bf16 norm weight.
+        """
+        if tuple(norm.normalized_shape) != (self.dim,):
+            raise ValueError(f"norm must normalise the last dimension {self.dim} (got {norm.normalized_shape})")
+        shape = x.shape
+        flat = x.view(-1, self.dim)
+        if not flat.is_cuda:
+            raise RuntimeError("fusionllm_amd.DeepSeekMoE runs on a ROCm device only (got a CPU tensor)")
+        nw = norm.weight
+        if nw is not None and flat.dtype == torch.bfloat16 and nw.dtype != torch.bfloat16:
+            raise NotImplementedError("a bf16 input needs a bf16 RMSNorm weight")
+        if nw is not None and nw.device != flat.device:
+            raise RuntimeError("the RMSNorm weight must be on the input's device")
+        weights = self._flat_weights()
+        out_dtype = self._output_dtype(flat, weights)
+        if flat.shape[0] == 0:
+            return x + self.forward(norm(x))  # zero tokens: empty tensors only
+        eps = norm.eps if norm.eps is not None else torch.finfo(flat.dtype).eps
+        return self._run(flat, weights, out_dtype, norm_w=nw, eps=float(eps), fused_norm=True).view(shape)
+
+    def _run(self, flat, weights, out_dtype, norm_w=None, eps=0.0, fused_norm=False):
+        E, k = self.n_routed_experts, self.n_activated_experts
         meta = (E, k, self.moe_inter_dim, float(self.route_scale), self.shared_expert is not None, out_dtype)
         needs_grad = torch.is_grad_enabled() and (
             flat.requires_grad or self.gate.weight.requires_grad or self.gate.bias.requires_grad
-            or any(t.requires_grad for t in weights))
+            or any(t.requires_grad for t in weights) or (norm_w is not None and norm_w.requires_grad))
         # Switch devices only when needed (the context manager costs host time).
         switch = flat.device.index != torch._C._cuda_getDevice()
         with torch.cuda.device(flat.device) if switch else contextlib.nullcontext():
-            if needs_grad:
+            if needs_grad and fused_norm:
+                y, idx64, w, counts = _NormMoEResidualFunction.apply(
+                    meta, eps, flat, norm_w, self.gate.weight, self.gate.bias, *weights)
+            elif needs_grad:
                 y, idx64, w, counts = _MoEBlockFunction.apply(meta, flat, self.gate.weight, self.gate.bias,
                                                               *weights)
             else:
                 # inference: the same kernels, nothing kept for a backward pass
-                fw = _forward_pass(meta, flat, self.gate.weight, self.gate.bias, weights)
+                x_in, residual = flat, None
+                if fused_norm:
+                    residual = flat.contiguous()
+                    x_in, _ = K.rmsnorm_fwd(residual, None if norm_w is None else norm_w.contiguous(), eps)
+                fw = _forward_pass(meta, x_in, self.gate.weight, self.gate.bias, weights, residual)
                 idx64, w, counts, y = fw[4], fw[5], fw[7], fw[-1]
         self._last_indices = idx64
         self._last_weights = w
         self._last_counts, self._counts_of = counts, idx64
-        return y.view(shape)
+        return y
 
     def _forward_empty(self, flat: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
         # Zero tokens: nothing to compute.  Keep the output connected to the
@@ -303,3 +397,13 @@ class DeepSeekMoE(nn.Module):
         prob = torch.zeros(T, E, dtype=w.dtype, device=w.device).scatter_add_(
             1, self._last_indices.reshape(T, k), w.reshape(T, k)).mean(dim=0)
         return (frac * prob).sum() * E
+
+
+def moe_residual(x: torch.Tensor, norm: nn.Module, moe: nn.Module) -> torch.Tensor:
+    """``x + moe(norm(x))``, the FFN half of FusionLLMBlock.forward
+    (models/fusionllm.py:52).  A fusionllm_amd ``DeepSeekMoE`` after an
+    ``nn.RMSNorm`` runs fused (norm, MoE and residual add in the kernels);
+    any other pair runs as the plain expression."""
+    if isinstance(moe, DeepSeekMoE) and isinstance(norm, nn.RMSNorm) and x.is_cuda:
+        return moe.forward_norm_residual(x, norm)
+    return x + moe(norm(x))

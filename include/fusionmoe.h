@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define FMOE_ABI_VERSION 3
+#define FMOE_ABI_VERSION 4
 #define FMOE_MAX_EXPERTS 64
 #define FMOE_MAX_TOPK 8
 
@@ -142,13 +142,17 @@ int fmoe_down_fwd(const void* h, const int32_t* offsets, int n_experts,
  *   acc = 0; acc = acc + (o_j * w_j)  (product rounded, then the add)
  * then y = out_dtype(acc) + shared (bf16 add for FMOE_BF16; for FMOE_F32 the
  * fp32 sum acc + shared, the autocast case where x is fp32).
+ * With a residual (nullable, [T, dim] of out_dtype) the output is the FFN half
+ * of FusionLLMBlock.forward, x + ffn(norm2(x)) (models/fusionllm.py:52):
+ * y = residual + out_dtype(y_moe), added in out_dtype.
  * Deterministic: token-major gather, no atomics.
  * expert_out: [rows_routed + rows_shared, dim] bf16 (from fmoe_down_fwd).
  * ------------------------------------------------------------------------- */
 int fmoe_combine_fwd(const void* expert_out, const int32_t* idx,
                      const float* weights, const int32_t* pos_of_slot,
                      int64_t T, int64_t dim, int k, int64_t rows_routed,
-                     int has_shared, int out_dtype, void* y, void* stream);
+                     int has_shared, int out_dtype, const void* residual,
+                     void* y, void* stream);
 
 /* Backward of the combine (autograd of moe.py:76-77,87):
  *   d_expert_out[r] = bf16(dy[t] * w_slot)   for routed row r (slot perm[r]),
@@ -238,6 +242,41 @@ int fmoe_dx_reduce(const void* dx_rows, const int32_t* pos_of_slot,
                    const void* gate_w, int64_t T, int64_t dim, int k,
                    int64_t rows_routed, int has_shared, int out_dtype,
                    void* dx, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * RMSNorm around the block: FusionLLMBlock's FFN half x + ffn(norm2(x)) with
+ * norm2 = nn.RMSNorm(dim, eps=1e-6) (models/fusionllm.py:48,52; torch's
+ * F.rms_norm).  dim <= 4096.
+ *
+ * Forward: r[t] = 1 / sqrt(sum_c x[t,c]^2 / dim + eps) (fp32, correctly
+ * rounded sqrt and divide; the sum in a fixed lane order), then
+ * xn[t,c] = bf16((x[t,c] * r[t]) * norm_w[c]).  x: [T, dim] of x_dtype;
+ * norm_w: [dim] of w_dtype, or NULL for a norm without weight; xn: [T, dim]
+ * bf16, the MoE input; rstd: [T] fp32, kept for the backward.
+ * ------------------------------------------------------------------------- */
+int fmoe_rmsnorm_fwd(const void* x, int x_dtype, const void* norm_w, int w_dtype,
+                     int64_t T, int64_t dim, float eps, void* xn, float* rstd,
+                     void* stream);
+
+/* Workspace of fmoe_dx_reduce_norm when d_norm_w is wanted: 4160 fp32 rows
+ * of dim (4096 per-workgroup partial rows and 64 second-level rows). */
+size_t fmoe_norm_bwd_workspace_bytes(int64_t dim);
+
+/* Backward of x + moe(rmsnorm(x)): per token, d_xn as in fmoe_dx_reduce
+ * (fp32, not rounded), then
+ *   g = d_xn * norm_w,  xh = x * r,
+ *   dx = r * (g - xh * (sum_c g*xh) / dim) + d_out      (written in x_dtype)
+ * and d_norm_w[c] = sum_t d_xn[t,c] * xh[t,c] (w_dtype), reduced in a fixed
+ * order.  d_out and dx have x_dtype; d_norm_w may be NULL (no weight
+ * gradient; then the workspace may be NULL too). */
+int fmoe_dx_reduce_norm(const void* dx_rows, const int32_t* pos_of_slot,
+                        const int32_t* idx, const float* d_logits,
+                        const void* gate_w, int64_t T, int64_t dim, int k,
+                        int64_t rows_routed, int has_shared,
+                        const void* x, const float* rstd, const void* norm_w,
+                        int w_dtype, const void* d_out, int x_dtype, void* dx,
+                        void* d_norm_w, void* workspace, size_t workspace_bytes,
+                        void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,304 @@
+"""Parity of the fused FFN half of FusionLLMBlock on the GPU:
+out = x + DeepSeekMoE(RMSNorm(x))  (models/fusionllm.py:48,52; config C4).
+
+Reference: the torch-CPU restatement (oracle.moe_oracle: rms_norm = torch's
+F.rms_norm, the MoE composition of models/moe.py) in bf16 — the reference
+composition — and in fp64 on the same bf16 operands (ground truth), both run
+on the routing the GPU chose; the routing itself is checked bit-exact against
+the C router oracle on the GPU's own RMSNorm output.
+
+Tolerances (stated here, applied below):
+  xn (the MoE input)  within 1 bf16 ulp of torch's F.rms_norm and >= 99% of
+                      elements bitwise equal (the fp32 sum of squares is added
+                      in another order, which can move a rounding boundary)
+  rstd                relative 4e-6 to the fp64 closed form
+  out                 elementwise |d| <= 2e-3 + 2e-2 * max(|y|, |out|) + 1 bf16
+                      ulp of out against the bf16 reference composition, with
+                      y = the reference's MoE output inside the block: the
+                      north star's rtol 2e-2 / atol 2e-3 on the MoE output,
+                      carried through the residual add (where x and y cancel,
+                      y's error is kept in absolute terms) plus that add's
+                      bf16 rounding
+  dx                  as the MoE block's dx check (tests/test_gpu_moe.py) with
+                      k+3 terms per element: k routed experts, the shared
+                      expert, the router and the residual
+  weight gradients    relative L2 <= 1e-2 per tensor, the norm weight included
+C4 stack (16 layers): routing bit-exact in every layer (against the C router
+on that layer's GPU input); the output and dx against the bf16 reference run
+layer by layer on the GPU's routing, by relative L2 <= 1e-2 and within
+1.5x the bf16 reference's own distance to the fp64 truth (+1e-4): rounding
+differences compound over 16 residual layers, so an elementwise bound would
+measure the reference's rounding as much as the kernels'.  The weight
+gradients of the first and last layer: relative L2 to the truth <= 1e-2, or
+within 1.5x the bf16 reference's (+1e-4) where 15 layers of bf16 backward
+put the reference itself near 1e-2 (the gate weight's gradient is a sum of
+cancelling per-token terms).
+"""
+import pytest
+import torch
+import torch.nn as nn
+
+from fusionllm_amd import _kernels as K
+from fusionllm_amd import configs, moe_residual
+from oracle import moe_oracle as mo
+from tests.gpu_util import build_module, f32_bits, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+Y_TOL = dict(rtol=2e-2, atol=2e-3)
+DX_ATOL_PER_TERM = 2.5e-3
+DX_RTOL = 2e-2
+W_REL_L2 = 1e-2
+EPS = 1e-6  # nn.RMSNorm(dim, eps=1e-6), models/fusionllm.py:48
+
+C4_LAYER = configs.BlockConfig("C4-layer", 1024, bias="uniform:0.05")
+
+
+def _bf16_ulp_diff(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """|a - b| in units of bf16 ulps (ordered-integer distance)."""
+    def key(t):
+        i = t.contiguous().view(torch.int16).to(torch.int32)
+        return torch.where(i < 0, -(i & 0x7FFF), i)
+    return (key(a) - key(b)).abs()
+
+
+def _norm_weight(d, seed, dtype):
+    g = torch.Generator().manual_seed(1000 + seed)
+    return (1.0 + 0.1 * torch.randn(d, generator=g)).to(dtype)
+
+
+@pytest.mark.parametrize("d", [256, 768, 2048])
+@pytest.mark.parametrize("x_dtype,w_dtype", [(torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32),
+                                             (torch.float32, None)])
+def test_rmsnorm_fwd_against_torch(gpu_device, d, x_dtype, w_dtype):
+    g = torch.Generator().manual_seed(d)
+    T = 777
+    x = torch.randn(T, d, generator=g)
+    x[::7] *= 100.0   # large and small rows
+    x[1::7] *= 1e-3
+    x[5] = 0.0        # all-zero row: r = 1/sqrt(eps)
+    x = x.to(x_dtype)
+    w = None if w_dtype is None else _norm_weight(d, d, w_dtype)
+    xn, rstd = K.rmsnorm_fwd(x.to(gpu_device), None if w is None else w.to(gpu_device), EPS)
+    xn, rstd = xn.cpu(), rstd.cpu()
+    want = mo.rms_norm(x, w, EPS).bfloat16()  # torch's F.rms_norm, then the MoE's bf16 input cast
+    ulps = _bf16_ulp_diff(xn, want)
+    assert int(ulps.max()) <= 1, f"max {int(ulps.max())} ulps"
+    assert float((ulps == 0).double().mean()) >= 0.99
+    x64 = x.double()
+    r64 = 1.0 / torch.sqrt((x64 * x64).mean(-1) + EPS)
+    assert torch.allclose(rstd.double(), r64, rtol=4e-6, atol=0)
+
+
+def _gpu_block(cfg, data, nw, dev, backward=True, dtype=torch.bfloat16):
+    m = build_module(cfg, data, dev, dtype=dtype)
+    norm = nn.RMSNorm(cfg.dim, eps=EPS).to(device=dev, dtype=dtype)
+    with torch.no_grad():
+        norm.weight.copy_(nw)
+    x = data.x.to(dev, dtype).requires_grad_(backward)
+    out = moe_residual(x, norm, m)
+    res = {"out": out.detach().cpu(), "idx": m._last_indices.cpu(), "w": m._last_weights.cpu(),
+           "x": x.detach()}
+    if backward:
+        out.backward(data.dy.to(dev, dtype))
+        res["dx"] = x.grad.cpu()
+        res["grads"] = {n: (p.grad.cpu() if p.grad is not None else None) for n, p in m.named_parameters()}
+        res["grads"]["norm.weight"] = norm.weight.grad.cpu()
+    return res
+
+
+def _oracle_block(cfg, data, nw, idx_gpu, backward=True, dtype=torch.bfloat16, x=None):
+    """x + moe(rms_norm(x)) on the CPU, on the GPU's routing (dtype bf16: the
+    reference composition; fp64: ground truth on the bf16 operands)."""
+    sd = {k: v.bfloat16().to(dtype).clone().requires_grad_(backward) for k, v in data.state_dict().items()}
+    sd["norm.weight"] = nw.bfloat16().to(dtype).clone().requires_grad_(backward)
+    x = (data.x if x is None else x).bfloat16().to(dtype).clone().requires_grad_(backward)
+    E, k = cfg.n_experts, cfg.topk
+    experts = [(sd[f"experts.{e}.w1.weight"], sd[f"experts.{e}.w3.weight"], sd[f"experts.{e}.w2.weight"])
+               for e in range(E)]
+    shared = (sd["shared_expert.w1.weight"], sd["shared_expert.w3.weight"], sd["shared_expert.w2.weight"])
+    xn = mo.rms_norm(x, sd["norm.weight"], EPS)
+    w, idx = mo.route(xn, sd["gate.weight"], sd["gate.bias"], k, cfg.route_scale, mode="fp32", indices=idx_gpu)
+    acc = torch.float64 if dtype == torch.float64 else torch.float32
+    y, _, _ = mo.moe_forward(xn, sd["gate.weight"], sd["gate.bias"], experts, shared, k, cfg.route_scale,
+                             routing=(w, idx), acc_dtype=acc)
+    out = x + y
+    res = {"out": out.detach(), "y": y.detach(), "x": x}
+    if backward:
+        out.backward(data.dy.bfloat16().to(dtype))
+        res["dx"] = x.grad
+        res["grads"] = {n: t.grad for n, t in sd.items()}
+    return res
+
+
+def _bf16_ulp(t: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 values at |t| (2^(e-7) for |t| in [2^e, 2^(e+1)))."""
+    m = t.double().abs().clamp_min(2.0 ** -126)
+    return torch.exp2(torch.floor(torch.log2(m)) - 7)
+
+
+def _check_out(out_gpu, ref):
+    a, b, y = out_gpu.double().cpu(), ref["out"].double(), ref["y"].double()
+    err = (a - b).abs()
+    bound = Y_TOL["atol"] + Y_TOL["rtol"] * torch.maximum(y.abs(), b.abs()) + _bf16_ulp(b)
+    bad = err > bound
+    assert not bad.any(), (f"out: {int(bad.sum())}/{bad.numel()} elements beyond tolerance; "
+                           f"max abs err {float(err.max()):.3e}")
+
+
+def _check_dx(dx_gpu, dx_ref, truth, terms):
+    a, r, t = dx_gpu.double().cpu(), dx_ref.double().cpu(), truth.double().cpu()
+    err = (a - t).abs()
+    bad = err > (r - t).abs() + terms * DX_ATOL_PER_TERM + DX_RTOL * t.abs()
+    assert not bad.any(), (f"dx: {int(bad.sum())}/{bad.numel()} elements beyond tolerance; "
+                           f"max abs err {float(err.max()):.3e}")
+    e_gpu, e_ref = rel_l2(a, t), rel_l2(r, t)
+    assert e_gpu <= 1e-2, f"dx relative L2 to fp64 truth {e_gpu:.3e}"
+    assert e_gpu <= 1.5 * e_ref + 1e-4, f"dx rel L2 {e_gpu:.3e} vs the bf16 reference's {e_ref:.3e}"
+
+
+def _routing_exact_on_gpu_xn(cfg, data, nw, g, dev):
+    xn, _ = K.rmsnorm_fwd(g["x"].contiguous(), nw.to(dev), EPS)
+    ridx, rw, _ = mo.router_c(xn.cpu(), data.gate_w.bfloat16(), data.gate_b.bfloat16(), cfg.topk,
+                              cfg.route_scale)
+    assert torch.equal(g["idx"], ridx.long())
+    assert torch.equal(f32_bits(g["w"]), f32_bits(rw))
+    return xn
+
+
+@pytest.mark.parametrize("T", [1024, 333])
+def test_norm_block_forward_backward(gpu_device, T):
+    cfg = C4_LAYER
+    data = configs.make_block(cfg, seed=2, tokens=T)
+    nw = _norm_weight(cfg.dim, 2, torch.bfloat16)
+    g = _gpu_block(cfg, data, nw, gpu_device)
+    _routing_exact_on_gpu_xn(cfg, data, nw, g, gpu_device)
+    o = _oracle_block(cfg, data, nw, g["idx"])
+    _check_out(g["out"], o)
+    truth = _oracle_block(cfg, data, nw, g["idx"], dtype=torch.float64)
+    _check_dx(g["dx"], o["dx"], truth["dx"], cfg.topk + 3)
+    for name, ref in o["grads"].items():
+        got = g["grads"][name]
+        if ref is None:
+            assert got is None, name
+            continue
+        assert got is not None and got.dtype == torch.bfloat16, name
+        err = rel_l2(got, ref)
+        assert err <= W_REL_L2, f"{name}: relative L2 error {err:.3e}"
+    assert rel_l2(g["grads"]["norm.weight"], truth["grads"]["norm.weight"]) <= W_REL_L2
+
+
+def test_norm_block_inference_matches_training_path(gpu_device):
+    cfg = C4_LAYER
+    data = configs.make_block(cfg, seed=3, tokens=512)
+    nw = _norm_weight(cfg.dim, 3, torch.bfloat16)
+    g = _gpu_block(cfg, data, nw, gpu_device, backward=True)
+    with torch.no_grad():
+        h = _gpu_block(cfg, data, nw, gpu_device, backward=False)
+    assert torch.equal(g["out"].view(torch.int16), h["out"].view(torch.int16))
+    assert torch.equal(g["idx"], h["idx"])
+
+
+def test_norm_block_autocast_fp32_matches_unfused(gpu_device):
+    # Trainer mode (training/trainer.py:158): fp32 module and input under bf16
+    # autocast.  The fused path against the unfused composition
+    # x + moe(nn.RMSNorm(x)) with torch's own RMSNorm on the device.
+    cfg = configs.BlockConfig("autocast-norm", 512, dim=256, inter=512, n_experts=8, topk=2, bias="skew")
+    data = configs.make_block(cfg, seed=6)
+    nw = _norm_weight(cfg.dim, 6, torch.float32)
+    outs = []
+    for fused in (True, False):
+        m = build_module(cfg, data, gpu_device, dtype=torch.float32)
+        norm = nn.RMSNorm(cfg.dim, eps=EPS).to(gpu_device)
+        with torch.no_grad():
+            norm.weight.copy_(nw)
+        x = data.x.to(gpu_device).requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            out = moe_residual(x, norm, m) if fused else x + m(norm(x))
+        assert out.dtype == torch.float32
+        out.backward(data.dy.to(gpu_device))
+        grads = {n: p.grad for n, p in m.named_parameters()}
+        grads["norm.weight"] = norm.weight.grad
+        outs.append((out.detach(), x.grad, grads, m._last_indices.clone()))
+    (a, dxa, ga, ia), (b, dxb, gb, ib) = outs
+    assert torch.equal(ia, ib)  # same routing (xn within an ulp; no near-ties at this seed)
+    x = data.x.to(gpu_device)
+    _check_out(a, {"out": b.cpu(), "y": (b - x).cpu()})
+    assert rel_l2(dxa, dxb) <= W_REL_L2
+    for n in ga:
+        assert (ga[n] is None) == (gb[n] is None), n
+        if ga[n] is not None:
+            assert ga[n].dtype == torch.float32
+            assert rel_l2(ga[n], gb[n]) <= W_REL_L2, n
+
+
+def test_c4_stack_of_16_layers(gpu_device):
+    # C4: 16 x (RMSNorm + MoE + residual), independent seeded weights per
+    # layer, bias U(-0.05, 0.05), bf16 forward + backward; 1024 tokens here
+    # (the full [4, 4096, 768] runs in bench.py --config C4).
+    cfg = configs.C4
+    L, T = cfg.layers, 1024
+    layers = [configs.make_block(cfg, seed=100 + l, tokens=T, with_dy=False) for l in range(L)]
+    nws = [_norm_weight(cfg.dim, 100 + l, torch.bfloat16) for l in range(L)]
+    x0 = configs.make_block(cfg, seed=99, tokens=T, experts=False).x
+    dy = configs.make_block(cfg, seed=98, tokens=T, experts=False).x
+    mods, norms = [], []
+    for data, nw in zip(layers, nws):
+        mods.append(build_module(cfg, data, gpu_device))
+        n = nn.RMSNorm(cfg.dim, eps=EPS).to(device=gpu_device, dtype=torch.bfloat16)
+        with torch.no_grad():
+            n.weight.copy_(nw)
+        norms.append(n)
+    x = x0.to(gpu_device, torch.bfloat16).requires_grad_(True)
+    h, ins, routing = x, [], []
+    for m, n in zip(mods, norms):
+        ins.append(h.detach())
+        h = moe_residual(h, n, m)
+        routing.append(m._last_indices.cpu())
+    h.backward(dy.to(gpu_device, torch.bfloat16))
+    out_gpu, dx_gpu = h.detach().cpu(), x.grad.cpu()
+
+    # Routing bit-exact in every layer, on that layer's GPU input.
+    for l in range(L):
+        xn, _ = K.rmsnorm_fwd(ins[l].contiguous(), nws[l].to(gpu_device), EPS)
+        ridx, _, _ = mo.router_c(xn.cpu(), layers[l].gate_w.bfloat16(), layers[l].gate_b.bfloat16(),
+                                 cfg.topk, cfg.route_scale)
+        assert torch.equal(routing[l], ridx.long()), f"layer {l}"
+
+    def oracle_stack(dtype):
+        xo = x0.bfloat16().to(dtype).clone().requires_grad_(True)
+        hh, params = xo, []
+        for l in range(L):
+            data = layers[l]
+            sd = {k: v.bfloat16().to(dtype).clone().requires_grad_(True) for k, v in data.state_dict().items()}
+            nw = nws[l].to(dtype).clone().requires_grad_(True)
+            params.append((sd, nw))
+            experts = [(sd[f"experts.{e}.w1.weight"], sd[f"experts.{e}.w3.weight"],
+                        sd[f"experts.{e}.w2.weight"]) for e in range(cfg.n_experts)]
+            shared = (sd["shared_expert.w1.weight"], sd["shared_expert.w3.weight"], sd["shared_expert.w2.weight"])
+            xn = mo.rms_norm(hh, nw, EPS)
+            w, idx = mo.route(xn, sd["gate.weight"], sd["gate.bias"], cfg.topk, 1.0, mode="fp32",
+                              indices=routing[l])
+            acc = torch.float64 if dtype == torch.float64 else torch.float32
+            y, _, _ = mo.moe_forward(xn, sd["gate.weight"], sd["gate.bias"], experts, shared, cfg.topk, 1.0,
+                                     routing=(w, idx), acc_dtype=acc)
+            hh = hh + y
+        hh.backward(dy.bfloat16().to(dtype))
+        return hh.detach(), xo.grad, params
+
+    out_ref, dx_ref, p_ref = oracle_stack(torch.bfloat16)
+    out_t, dx_t, p_t = oracle_stack(torch.float64)
+    for got, ref, t, what in ((out_gpu, out_ref, out_t, "out"), (dx_gpu, dx_ref, dx_t, "dx")):
+        e_gpu, e_ref = rel_l2(got, t), rel_l2(ref, t)
+        assert e_gpu <= 1e-2, f"{what}: relative L2 to fp64 truth {e_gpu:.3e}"
+        assert e_gpu <= 1.5 * e_ref + 1e-4, f"{what}: rel L2 {e_gpu:.3e} vs the bf16 reference's {e_ref:.3e}"
+    for l in (0, L - 1):
+        pairs = [(name, p.grad, p_ref[l][0][name].grad, p_t[l][0][name].grad)
+                 for name, p in mods[l].named_parameters()]
+        pairs.append(("norm.weight", norms[l].weight.grad, p_ref[l][1].grad, p_t[l][1].grad))
+        for name, got, ref, t in pairs:
+            assert (got is None) == (ref is None), (l, name)
+            if ref is None:
+                continue
+            e_gpu, e_ref = rel_l2(got.cpu(), t), rel_l2(ref, t)
+            assert e_gpu <= max(W_REL_L2, 1.5 * e_ref + 1e-4), (l, name, e_gpu, e_ref)

@@ -21,7 +21,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     syms = declared_symbols()
-    assert len(syms) == 18
+    assert len(syms) == 21
     for s in syms:
         assert hasattr(lib, s), s
     assert set(syms) == set(_lib.SIGNATURES), "ctypes binding and header disagree"
@@ -47,13 +47,27 @@ def test_argument_errors_without_gpu():
     pp = _lib.ptr_array([0])
     assert lib.fmoe_gateup_fwd(None, None, None, 1, 10, 0, 96, 128, pp, pp, None, None, None) == 2
     assert lib.fmoe_gateup_fwd(None, None, None, 1, 10, 0, 128, 128, pp, pp, None, None, None) == 1
-    assert lib.fmoe_combine_fwd(None, None, None, None, 4, 768, 2, 8, 1, 5, None, None) == 4
+    assert lib.fmoe_combine_fwd(None, None, None, None, 4, 768, 2, 8, 1, 5, None, None, None) == 4
+    # RMSNorm around the block
+    assert lib.fmoe_rmsnorm_fwd(None, 0, None, 0, 4, 100, 1e-6, None, None, None) == 2
+    assert lib.fmoe_rmsnorm_fwd(None, 0, None, 0, 4, 8192, 1e-6, None, None, None) == 2
+    assert lib.fmoe_rmsnorm_fwd(None, 5, None, 0, 4, 768, 1e-6, None, None, None) == 4
+    assert lib.fmoe_rmsnorm_fwd(None, 0, None, 0, 4, 768, 1e-6, None, None, None) == 1
+    assert lib.fmoe_rmsnorm_fwd(None, 0, None, 0, 0, 768, 1e-6, None, None, None) == 0
+    fake = 1 << 20  # a non-null address that is never dereferenced (rejected first)
+    assert lib.fmoe_dx_reduce_norm(None, None, None, None, None, 4, 768, 2, 8, 1, None, None, None, 0,
+                                   None, 0, None, fake, fake, 1 << 30, None) == 1  # d_norm_w without norm_w
+    assert lib.fmoe_dx_reduce_norm(None, None, None, None, None, 4, 768, 2, 8, 1, None, None, fake, 0,
+                                   None, 0, None, fake, fake, 100, None) == 6  # workspace too small
+    assert lib.fmoe_dx_reduce_norm(None, None, None, None, None, 4, 768, 2, 8, 1, None, None, None, 0,
+                                   None, 0, None, None, None, 0, None) == 1  # null inputs
     assert lib.fmoe_weight_grad(None, None, 8, None, None, 8, None, 1, 10, 0, 128, 128, 0, pp, None, 0,
                                 None, 0, None) == 2
     # size queries
     assert lib.fmoe_dispatch_workspace_bytes(16384, 8, 2) == 2 * 32 * 8 * 4
     assert lib.fmoe_weight_grad_workspace_bytes(32768, 16384, 8, 768, 2048) > 0
     assert lib.fmoe_router_bwd_workspace_bytes(16384, 768, 8, 2) == (16384 * 2 // 64 + 8) * 769 * 4
+    assert lib.fmoe_norm_bwd_workspace_bytes(768) == 4160 * 768 * 4
 
 
 def test_parameter_names_shapes_and_count():

@@ -238,3 +238,31 @@ def test_block_forward_residual_and_norm():
     xn = x / torch.sqrt((x * x).mean(-1, keepdim=True) + 1e-6)
     y, _, _ = mo.moe_forward(xn, gw, gb, ex, sh, 2)
     assert torch.allclose(out, x + y, rtol=1e-12, atol=1e-12)
+
+
+def test_rms_norm_is_torch_rms_norm_and_planted_mistakes_fail():
+    # oracle.rms_norm is nn.RMSNorm(dim, eps=1e-6) of models/fusionllm.py:48
+    # (F.rms_norm); fp64 closed form x / sqrt(mean(x^2) + eps) * w, and the
+    # 1-ulp bf16 check used against the kernel rejects a norm without its
+    # weight or without eps.
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(64, 768, generator=g, dtype=torch.float64)
+    w = 1.0 + 0.1 * torch.randn(768, generator=g, dtype=torch.float64)
+    want = x / torch.sqrt((x * x).mean(-1, keepdim=True) + 1e-6) * w
+    assert torch.allclose(mo.rms_norm(x, w), want, rtol=1e-13, atol=0)
+
+    def ulps(a, b):
+        def key(t):
+            i = t.contiguous().view(torch.int16).to(torch.int32)
+            return torch.where(i < 0, -(i & 0x7FFF), i)
+        return int((key(a) - key(b)).abs().max())
+
+    xb, wb = x.bfloat16(), w.bfloat16()
+    ref = mo.rms_norm(xb, wb, 1e-6)
+    x64, w64 = xb.double(), wb.double()
+    want = x64 / torch.sqrt((x64 * x64).mean(-1, keepdim=True) + 1e-6) * w64
+    assert ulps(ref, want.bfloat16()) <= 1
+    assert ulps(mo.rms_norm(xb, None, 1e-6), ref) > 1
+    xb[0] = 1e-4
+    ref = mo.rms_norm(xb, wb, 1e-6)
+    assert ulps(mo.rms_norm(xb, wb, 0.0)[0], ref[0]) > 1
