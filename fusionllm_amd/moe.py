@@ -5,7 +5,8 @@ Mirrors FusionLLM ``models/moe.py``:
   * ``SwiGLUExpert`` (moe.py:11-21) — same parameters (w1, w2, w3, bias-free
     nn.Linear) and the same forward; it is a parameter container for
     ``DeepSeekMoE`` and is also imported on its own by the reference's MTP
-    module (models/mtp.py:11,28), where it runs as plain torch.
+    module (models/mtp.py:11,28), where its forward runs the one-group
+    kernels (``dense_swiglu``), as does ``DenseFFN`` (models/fusionllm.py:17-27).
   * ``DeepSeekMoE`` (moe.py:24-109) — same constructor and config keys
     (moe.py:27-42), parameter names and init, ``forward`` (moe.py:79-87),
     ``update_gate_bias`` (moe.py:89-98), ``get_load_balance_loss``
@@ -35,8 +36,109 @@ import torch.nn.functional as F
 from . import _kernels as K
 
 
+def _as_bf16(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)
+
+
+_DENSE_OFFSETS: dict = {}
+
+
+def _dense_offsets(T: int, device: torch.device) -> torch.Tensor:
+    """Group offsets [0, T] (int32, on the device) of a one-group product."""
+    key = (T, device)
+    off = _DENSE_OFFSETS.get(key)
+    if off is None:
+        if len(_DENSE_OFFSETS) > 256:
+            _DENSE_OFFSETS.clear()
+        off = torch.tensor([0, T], dtype=torch.int32, device=device)
+        _DENSE_OFFSETS[key] = off
+    return off
+
+
+class _DenseSwiGLUFunction(torch.autograd.Function):
+    """w2(silu(w1 x) * w3 x) on the grouped kernels with one group of all T
+    rows (the dense FFN of models/fusionllm.py:17-27 and the SwiGLU of
+    models/moe.py:11-21 used on its own, models/mtp.py:28): the gate/up product
+    with the SiLU*up epilogue, the down product, and their backward (dX with
+    the SwiGLU backward fused, dW1/dW3/dW2).  Output bf16, as the bf16
+    Linears give; input and weight gradients in their own dtypes."""
+
+    @staticmethod
+    def forward(ctx, x, w1, w3, w2):
+        T, d = x.shape
+        inter = w1.shape[0]
+        xb = _as_bf16(x).contiguous()
+        w1b, w3b, w2b = (_as_bf16(w).contiguous() for w in (w1, w3, w2))
+        off = _dense_offsets(T, x.device)
+        ab, h = K.gateup_fwd(xb, None, off, 1, [w1b], [w3b], inter)
+        y = K.down_fwd(h, off, 1, T, 0, [w2b], d)
+        ctx.save_for_backward(xb, ab, h, w1b, w3b, w2b, off)
+        ctx.dtypes = (x.dtype, w1.dtype, w3.dtype, w2.dtype)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        xb, ab, h, w1b, w3b, w2b, off = ctx.saved_tensors
+        x_dtype, w1_dtype, w3_dtype, w2_dtype = ctx.dtypes
+        T, d = xb.shape
+        inter = w1b.shape[0]
+        dyb = _as_bf16(dy).contiguous()
+        w13t, w2t = K.transpose_weights([w1b], [w3b], [w2b])
+        d_ab = K.down_bwd_dx(dyb, None, off, 1, w2t, ab, inter)
+        dw2 = torch.empty(d, inter, dtype=w2_dtype, device=xb.device)
+        K.weight_grad(dyb, None, h, None, off, 1, T, 0, d, [dw2], None, w2_dtype, tag="w2")
+        dx = None
+        if ctx.needs_input_grad[0]:
+            dx = K.gateup_bwd_dx(d_ab, off, 1, T, 0, w13t, d)
+            if dx.dtype != x_dtype:
+                dx = dx.to(x_dtype)
+        dw1 = torch.empty(inter, d, dtype=w1_dtype, device=xb.device)
+        dw3 = torch.empty(inter, d, dtype=w1_dtype, device=xb.device)
+        K.weight_grad(d_ab, None, xb, None, off, 1, T, 0, inter, [dw1], [dw3], w1_dtype, tag="w13")
+        if w3_dtype != w1_dtype:
+            dw3 = dw3.to(w3_dtype)
+        return dx, dw1, dw3, dw2
+
+
+def dense_swiglu(x: torch.Tensor, w1: torch.Tensor, w3: torch.Tensor, w2: torch.Tensor) -> torch.Tensor:
+    """``w2(silu(w1 x) * w3 x)`` for bias-free nn.Linear weights (w1, w3
+    [inter, dim], w2 [dim, inter]) on the kernels; any leading shape of x.
+
+    bf16: a bf16 input with bf16 weights, or any input under
+    ``torch.autocast("cuda", dtype=torch.bfloat16)`` (output bf16, as the
+    reference's Linears give there).  ROCm tensors only.
+    """
+    dim = w1.shape[1]
+    shape = x.shape
+    flat = x.reshape(-1, dim)
+    if not flat.is_cuda:
+        raise RuntimeError("fusionllm_amd SwiGLU runs on a ROCm device only (got a CPU tensor)")
+    if torch.is_autocast_enabled("cuda"):
+        if torch.get_autocast_dtype("cuda") != torch.bfloat16:
+            raise NotImplementedError("fusionllm_amd SwiGLU supports bf16 autocast only")
+        if flat.dtype not in (torch.bfloat16, torch.float32):
+            raise NotImplementedError(f"unsupported input dtype {flat.dtype}")
+    elif not (flat.dtype == torch.bfloat16 and all(w.dtype == torch.bfloat16 for w in (w1, w3, w2))):
+        raise NotImplementedError(
+            "fusionllm_amd SwiGLU computes in bf16: use bf16 weights and input, or run under "
+            "torch.autocast('cuda', dtype=torch.bfloat16)")
+    if flat.shape[0] == 0:
+        y = flat.new_zeros(0, dim, dtype=torch.bfloat16)
+        return (y + (w1.sum() + w3.sum() + w2.sum()).to(y.dtype) * 0 + flat.sum().to(y.dtype) * 0).view(shape)
+    switch = flat.device.index != torch._C._cuda_getDevice()
+    with torch.cuda.device(flat.device) if switch else contextlib.nullcontext():
+        y = _DenseSwiGLUFunction.apply(flat, w1, w3, w2)
+    return y.view(*shape[:-1], w2.shape[0])
+
+
 class SwiGLUExpert(nn.Module):
-    """SwiGLU expert w2(silu(w1 x) * w3 x) (reference: models/moe.py:11-21)."""
+    """SwiGLU expert w2(silu(w1 x) * w3 x) (reference: models/moe.py:11-21).
+
+    Inside ``DeepSeekMoE`` it only holds the expert's parameters (the block
+    runs all experts in grouped kernels).  Called on its own (the reference's
+    MTP module does, models/mtp.py:28), its forward runs the one-group
+    kernels of ``dense_swiglu``.
+    """
 
     def __init__(self, dim: int, inter_dim: int):
         super().__init__()
@@ -45,11 +147,13 @@ class SwiGLUExpert(nn.Module):
         self.w3 = nn.Linear(dim, inter_dim, bias=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.w2(F.silu(self.w1(x)) * self.w3(x))
+        return dense_swiglu(x, self.w1.weight, self.w3.weight, self.w2.weight)
 
 
-def _as_bf16(t: torch.Tensor) -> torch.Tensor:
-    return t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)
+class DenseFFN(SwiGLUExpert):
+    """Dense SwiGLU FFN of the GDN layers (reference: models/fusionllm.py:17-27),
+    same parameters (w1, w2, w3) and forward as the reference, on the
+    one-group kernels."""
 
 
 def _forward_pass(meta, x, gate_w, gate_b, weights, residual=None):

@@ -166,8 +166,13 @@ def test_aux_outputs_match_reference_formulas_bitwise(dtype):
             assert torch.equal(m.gate.bias.detach(), want)
 
 
-def test_swiglu_expert_forward_matches_closed_form():
-    e = SwiGLUExpert(16, 32).double()
-    x = torch.randn(5, 16, dtype=torch.float64)
-    a, b = x @ e.w1.weight.T, x @ e.w3.weight.T
-    assert torch.allclose(e(x), (a * torch.sigmoid(a) * b) @ e.w2.weight.T)
+def test_swiglu_and_dense_ffn_interface():
+    # models/moe.py:11-21 and models/fusionllm.py:17-27: bias-free w1, w2, w3;
+    # the forward runs on the kernels only (a CPU tensor raises, no fallback).
+    from fusionllm_amd import DenseFFN
+    for cls in (SwiGLUExpert, DenseFFN):
+        e = cls(64, 128)
+        assert {n: tuple(p.shape) for n, p in e.named_parameters()} == {
+            "w1.weight": (128, 64), "w2.weight": (64, 128), "w3.weight": (128, 64)}
+        with pytest.raises(RuntimeError):
+            e(torch.randn(5, 64))
