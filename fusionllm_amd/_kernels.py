@@ -16,15 +16,18 @@ from . import _lib
 from ._lib import BF16, F32, check, ptr_array
 
 # Optional per-entry-point timing: when a dict is installed with
-# set_timer(), every wrapper records a pair of HIP events around its launches
-# on the current stream (the stream the kernels run on) and appends them
-# under its name.  Used by bench.py; off by default.
+# set_timer(), every wrapper (or only those named in ``only``) records a pair
+# of HIP events around its launches on the current stream (the stream the
+# kernels run on) and appends them under its name.  Used by bench.py; off by
+# default.
 _TIMER: dict | None = None
+_TIMER_ONLY: frozenset | None = None
 
 
-def set_timer(store: dict | None) -> None:
-    global _TIMER
+def set_timer(store: dict | None, only=None) -> None:
+    global _TIMER, _TIMER_ONLY
     _TIMER = store
+    _TIMER_ONLY = None if only is None else frozenset(only)
 
 
 def _timed(fn):
@@ -34,11 +37,14 @@ def _timed(fn):
     def wrapper(*args, tag: str | None = None, **kwargs):
         if _TIMER is None:
             return fn(*args, **kwargs)
+        key = name if tag is None else f"{name}:{tag}"
+        if _TIMER_ONLY is not None and key not in _TIMER_ONLY:
+            return fn(*args, **kwargs)
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         out = fn(*args, **kwargs)
         end.record()
-        _TIMER.setdefault(name if tag is None else f"{name}:{tag}", []).append((start, end))
+        _TIMER.setdefault(key, []).append((start, end))
         return out
     return wrapper
 

@@ -290,6 +290,26 @@ __device__ __forceinline__ void split_item(const SplitPlan& sp, int nk, int item
   }
 }
 
+// 16-byte global store / load; nt marks data streamed through once (the
+// SwiGLU activations a|b and h, read again only in the backward pass, and
+// their gradient), so it does not displace operands from the caches.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store16(uint16_t* p, const uint4& v, bool nt) {
+  if (nt) {
+    const u32x4 q = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(q, reinterpret_cast<u32x4*>(p));
+  } else {
+    *reinterpret_cast<uint4*>(p) = v;
+  }
+}
+__device__ __forceinline__ uint4 load16(const uint16_t* p, bool nt) {
+  if (nt) {
+    const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(q.x, q.y, q.z, q.w);
+  }
+  return *reinterpret_cast<const uint4*>(p);
+}
+
 template <int MODE>
 __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs args,
                                                                  const int32_t* __restrict__ offsets) {
@@ -477,16 +497,15 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
             // columns 0..63: a, 64..127: b for h columns col0 .. col0 + 63
             const int hc = col0 + (c & 7) * 8;
             if (full || (lrow < rows_valid && hc < args.N)) {
-              uint16_t* dst = args.c0 + grow * args.ldc0 + (c < 8 ? 0 : args.inter) + hc;
-              *reinterpret_cast<uint4*>(dst) = v;
+              store16(args.c0 + grow * args.ldc0 + (c < 8 ? 0 : args.inter) + hc, v, true);
             }
           } else if constexpr (MODE == DOWN_BWD) {
             // h = s * b, s = bf16(silu(a)); dh arrives bf16-rounded:
             // da = bf16(bf16(dh * b) * silu'(a)), db = bf16(dh * s)
             const int hc = col0 + c * 8;
             if (full || (lrow < rows_valid && hc < args.N)) {
-              const uint4 avv = *reinterpret_cast<const uint4*>(args.aux + grow * args.ldaux + hc);
-              const uint4 bvv = *reinterpret_cast<const uint4*>(args.aux + grow * args.ldaux + args.inter + hc);
+              const uint4 avv = load16(args.aux + grow * args.ldaux + hc, true);
+              const uint4 bvv = load16(args.aux + grow * args.ldaux + args.inter + hc, true);
               float dh[8], af[8], bfv[8], da[8], db[8];
               unpack8(v, dh);
               unpack8(avv, af);
@@ -499,8 +518,8 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
                 da[e] = ds * (sg * (1.0f + af[e] * (1.0f - sg)));
                 db[e] = dh[e] * sv;
               }
-              *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + hc) = pack8(da);
-              *reinterpret_cast<uint4*>(args.c0 + grow * args.ldc0 + args.inter + hc) = pack8(db);
+              store16(args.c0 + grow * args.ldc0 + hc, pack8(da), true);
+              store16(args.c0 + grow * args.ldc0 + args.inter + hc, pack8(db), true);
             }
           } else {
             const int oc = col0 + c * 8;
@@ -535,7 +554,7 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
             const int lrow = wm * WTM + i * 16 + rr;
             const int hc = col0 + c * 8;
             if (full || (lrow < rows_valid && hc < args.N))
-              *reinterpret_cast<uint4*>(args.c1 + (grow0 + i * 16 + rr) * args.ldc1 + hc) = v;
+              store16(args.c1 + (grow0 + i * 16 + rr) * args.ldc1 + hc, v, true);
           }
         }
       }
