@@ -473,6 +473,20 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
       const int64_t grow0 = static_cast<int64_t>(row_base) + tm * BM + wm * WTM;
   #pragma unroll
       for (int i = 0; i < FM; ++i) {
+        // DOWN_BWD: a|b of the 16 rows go in flight before the staging below,
+        // all 8 loads at once (rows and columns clamped into the tile, so the
+        // addresses stay valid for a partial tile; such values are not stored)
+        uint4 pa[4], pb[4];
+        if constexpr (MODE == DOWN_BWD) {
+  #pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int r = t * 4 + (el >> 4), c = el & 15;
+            const int64_t growc = grow0 - wm * WTM + min(wm * WTM + i * 16 + r, rows_valid - 1);
+            const uint16_t* src = args.aux + growc * args.ldaux + min(col0 + c * 8, args.N - 8);
+            pa[t] = load16(src, true);
+            pb[t] = load16(src + args.inter, true);
+          }
+        }
         // stage rows 16 i .. 16 i + 15 of the wave block, 128 accumulator columns
         // (256 bytes per row; chunk c of row r at slot c ^ r)
         {
@@ -504,12 +518,10 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
             // da = bf16(bf16(dh * b) * silu'(a)), db = bf16(dh * s)
             const int hc = col0 + c * 8;
             if (full || (lrow < rows_valid && hc < args.N)) {
-              const uint4 avv = load16(args.aux + grow * args.ldaux + hc, true);
-              const uint4 bvv = load16(args.aux + grow * args.ldaux + args.inter + hc, true);
               float dh[8], af[8], bfv[8], da[8], db[8];
               unpack8(v, dh);
-              unpack8(avv, af);
-              unpack8(bvv, bfv);
+              unpack8(pa[t], af);
+              unpack8(pb[t], bfv);
   #pragma unroll
               for (int e = 0; e < 8; ++e) {
                 const float sg = fast_sigmoid(af[e]);
@@ -903,7 +915,21 @@ __global__ __launch_bounds__(core::NT, 1) void wgrad_tr_kernel(const WgradArgs a
   }
   if (g >= G) return;
   const int chunk = unit / tiles, tile = unit - chunk * tiles;
-  const int tm = tile / tiles_n, tn = tile - tm * tiles_n;
+  int tm = tile / tiles_n, tn = tile - tm * tiles_n;
+  if (tiles % 8 == 0) {
+    // A chunk's units start at a multiple of 8, so workgroup b runs on XCD
+    // tile % 8 (workgroups go to the 8 XCDs round-robin).  Each XCD takes whole
+    // column blocks of one operand (its L2 then serves them to all of that
+    // XCD's tiles of the chunk) and the same share of every chunk.
+    const int xcd = tile & 7, j = tile >> 3;
+    if (tiles_m % 8 == 0) {
+      tm = xcd + 8 * (j / tiles_n);
+      tn = j % tiles_n;
+    } else if (tiles_n % 8 == 0) {
+      tn = xcd + 8 * (j / tiles_m);
+      tm = j % tiles_m;
+    }
+  }
   const int m0 = tm * BM, n0 = tn * BN;
   const int k_begin = chunk * args.kc;
   const int k_end = min(M, k_begin + args.kc);
