@@ -353,7 +353,7 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
   // Copy instruction i of wave w writes LDS rows 64 i + 8 w .. +7 of an operand;
   // lane l fetches row 64 i + drow, global chunk dchunk (the swizzled slot l % 8).
   const int drow = w * 8 + (lane >> 3);
-  const int dchunk = (lane & 7) ^ swz(drow);  // swz(64 i + drow) == swz(drow)
+  const int dchunk = (lane & 7) ^ swzk(drow);  // swzk(64 i + drow) == swzk(drow)
   const uint32_t lds_copy = sbase + w * 1024;
   int c_ti = 0, c_kt = 0, c_k0 = 0, c_kn = 0;  // item ordinal, step within it, its K range
   const uint16_t* c_a = nullptr;   // A rows of the tile being copied
@@ -410,9 +410,9 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
   bf16x8 P[FN], Q[2][4];
 #pragma unroll
   for (int p = 0; p < FN; ++p)
-    P[p] = *reinterpret_cast<const bf16x8*>(smem + A_BYTES + ((xb ^ ((p & 3) << 5)) + 2048u * p));
+    P[p] = *reinterpret_cast<const bf16x8*>(smem + A_BYTES + (xb + 2048u * p));
 #pragma unroll
-  for (int q = 0; q < 4; ++q) Q[0][q] = *reinterpret_cast<const bf16x8*>(smem + ((xa ^ ((q & 3) << 5)) + 2048u * q));
+  for (int q = 0; q < 4; ++q) Q[0][q] = *reinterpret_cast<const bf16x8*>(smem + (xa + 2048u * q));
 
   f32x4 acc[FM][FN];
 #pragma unroll

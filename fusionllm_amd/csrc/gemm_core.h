@@ -38,6 +38,13 @@ constexpr int WTM = BM / WM, WTN = BN / WN; // 64 x 128 per wave
 constexpr int FM = WTM / 16, FN = WTN / 16; // 4 x 8 blocks of 16 x 16
 constexpr int LA = 4, LB = 4, LT = LA + LB; // copy instructions per lane per stage
 
+// Operand stages: 16-byte chunk c of 128-byte row r sits at slot c ^ swzk(r).
+// With this swizzle the fragment reads below (lane l: row l % 16 of a
+// 16-row group, chunk l / 16 [+4]) are free of LDS bank conflicts on gfx950
+// (measured with SQ_LDS_BANK_CONFLICT; folding bit 3 of the row into the
+// swizzle gave 2-way conflicts).
+__device__ __forceinline__ int swzk(int r) { return r & 7; }
+// Epilogue staging of 128-byte rows: slot c ^ swz(r).
 __device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -103,16 +110,16 @@ __device__ __forceinline__ void block8(f32x4& c00, f32x4& c01, f32x4& c02, f32x4
 
 // LDS address of fragment f of one operand: the lane's row (16 f + l % 16 of
 // the wave's block) at chunk (l / 16 + 4 * step half), swizzled.  For rows
-// r = base + 16 f + l % 16 with base % 64 == 0, swz(r) = (l & 7) ^ (2 (f & 3) + bit 3 of l),
-// so every fragment address is x ^ ((f & 3) << 5) + 2048 f for one per-lane x
-// (the wave's row block and l's swizzle), and the K half is one more XOR of 64.
+// r = base + 16 f + l % 16 with base % 16 == 0, swzk(r) = l & 7, so every
+// fragment address is x + 2048 f for one per-lane x (the wave's row block and
+// l's swizzle), and the K half is one XOR of 64 (chunk bit 2).
 __device__ __forceinline__ uint32_t frag_base(int row0, int lane) {
-  const int t = (lane >> 4) ^ (lane & 7) ^ ((lane >> 3) & 1);
+  const int t = (lane >> 4) ^ (lane & 7);
   return static_cast<uint32_t>((row0 + (lane & 15)) * RB + (t << 4));
 }
 template <int F, int KX>
 __device__ __forceinline__ uint32_t frag_addr(uint32_t x, uint32_t src) {
-  return (x ^ static_cast<uint32_t>(((F & 3) << 5) ^ KX)) + (src + 2048u * F);
+  return (x ^ static_cast<uint32_t>(KX)) + (src + 2048u * F);
 }
 
 // One 32-deep K step of the wave's 64 x 128 sub-tile on fragments P (B side,
