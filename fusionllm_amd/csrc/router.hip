@@ -138,11 +138,17 @@ __global__ __launch_bounds__(512) void router_fwd_kernel(
 //   dq_j = dw_j * rs;  dv_j = dq_j / D + dS,  dS = -sum_j dq_j * v_j / D^2;
 // top-k backward routes dv_j to the selected score; sigmoid backward gives
 //   dlogit_j = dv_j * (1 - v_j) * v_j.
+// One thread per expert-contiguous row r (slot perm[r] = t*k + j): the
+// normalisation and sigmoid backward of that slot, written by slot (for the
+// input gradient) and by row (for the gate reduction below, which then reads
+// it contiguously).  The token's sums run over j in ascending order.
 __global__ __launch_bounds__(256) void router_dlogit_kernel(
-    const float* __restrict__ dw, const float* __restrict__ v, int T, int k, float rs,
-    float* __restrict__ dl) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= T) return;
+    const float* __restrict__ dw, const float* __restrict__ v, const int32_t* __restrict__ perm,
+    int n_rows, int k, float rs, float* __restrict__ dl, float* __restrict__ dl_row) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= n_rows) return;
+  const int slot = perm[r];
+  const int t = slot / k, jr = slot - t * k;
   const float* dwt = dw + static_cast<int64_t>(t) * k;
   const float* vt = v + static_cast<int64_t>(t) * k;
   float sum = vt[0];
@@ -153,30 +159,30 @@ __global__ __launch_bounds__(256) void router_dlogit_kernel(
     const float dq = dwt[j] * rs;
     dS = dS - (dq * vt[j]) / (D * D);
   }
-  for (int j = 0; j < k; ++j) {
-    const float dq = dwt[j] * rs;
-    const float dv = dq / D + dS;
-    dl[static_cast<int64_t>(t) * k + j] = (dv * (1.0f - vt[j])) * vt[j];
-  }
+  const float dq = dwt[jr] * rs;
+  const float dv = dq / D + dS;
+  const float g = (dv * (1.0f - vt[jr])) * vt[jr];
+  dl[slot] = g;
+  dl_row[r] = g;
 }
 
 // Gate weight/bias gradient as a segmented column reduction over the
-// expert-contiguous rows:  dWg[e] = sum_{r in e} dl[perm[r]] * x_perm[r],
-// dbg[e] = sum_{r in e} dl[perm[r]].  Expert e's rows are cut into
+// expert-contiguous rows:  dWg[e] = sum_{r in e} dl_row[r] * x_perm[r],
+// dbg[e] = sum_{r in e} dl_row[r].  Expert e's rows are cut into
 // ceil(M_e / kChunkRows) chunks, numbered consecutively over the experts
 // (chunk_base(e) = sum of the chunk counts of experts < e).  Stage 1: one
-// block per chunk reduces its rows into partial[chunk][dim+1].  Stage 2 adds
-// the chunks of each expert in chunk order.  Both orders are fixed.
-constexpr int kChunkRows = 64;
+// block per chunk reduces its rows into partial[chunk][dim+1], row by row in
+// order (loads issued 8 rows at a time).  Stage 2 adds the chunks of each
+// expert in chunk order.  Both orders are fixed.
+constexpr int kChunkRows = 32;
 
 __device__ __forceinline__ int expert_chunks(const int32_t* offsets, int e) {
   return (offsets[e + 1] - offsets[e] + kChunkRows - 1) / kChunkRows;
 }
 
 __global__ __launch_bounds__(128) void router_wgrad_partial_kernel(
-    const float* __restrict__ dl, const int32_t* __restrict__ perm,
-    const int32_t* __restrict__ offsets, int E, const uint16_t* __restrict__ x_perm, int dim,
-    float* __restrict__ partial) {
+    const float* __restrict__ dl_row, const int32_t* __restrict__ offsets, int E,
+    const uint16_t* __restrict__ x_perm, int dim, float* __restrict__ partial) {
   int c = blockIdx.x, e = 0;
   for (; e < E; ++e) {
     const int n = expert_chunks(offsets, e);
@@ -191,20 +197,31 @@ __global__ __launch_bounds__(128) void router_wgrad_partial_kernel(
   for (int col8 = threadIdx.x; col8 <= nchunk8; col8 += blockDim.x) {
     if (col8 == nchunk8) {  // bias column
       float acc = 0.0f;
-      for (int r = r0; r < r1; ++r) acc = acc + dl[perm[r]];
+      for (int r = r0; r < r1; ++r) acc = acc + dl_row[r];
       out[dim] = acc;
-    } else {
-      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      for (int r = r0; r < r1; ++r) {
-        const float g = dl[perm[r]];
-        float xf[8];
-        unpack8(reinterpret_cast<const uint4*>(x_perm + static_cast<int64_t>(r) * dim)[col8], xf);
+      continue;
+    }
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int rb = r0; rb < r1; rb += 8) {
+      float g[8];
+      uint4 xv[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = fmaf(g, xf[i], acc[i]);
+      for (int u = 0; u < 8; ++u) {
+        const int r = min(rb + u, r1 - 1);  // rows past r1 get g = 0
+        g[u] = rb + u < r1 ? dl_row[r] : 0.0f;
+        xv[u] = reinterpret_cast<const uint4*>(x_perm + static_cast<int64_t>(r) * dim)[col8];
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) out[col8 * 8 + i] = acc[i];
+      for (int u = 0; u < 8; ++u) {
+        if (rb + u >= r1) break;
+        float xf[8];
+        unpack8(xv[u], xf);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = fmaf(g[u], xf[i], acc[i]);
+      }
     }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[col8 * 8 + i] = acc[i];
   }
 }
 
@@ -297,7 +314,8 @@ inline int64_t router_max_chunks(int64_t T, int n_experts, int k) {
 
 extern "C" size_t fmoe_router_bwd_workspace_bytes(int64_t T, int64_t dim, int n_experts, int k) {
   if (T <= 0 || dim <= 0 || n_experts <= 0 || k <= 0) return 0;
-  return static_cast<size_t>(router_max_chunks(T, n_experts, k) * (dim + 1)) * sizeof(float);
+  // chunk partials, then the per-row logit gradients
+  return static_cast<size_t>(router_max_chunks(T, n_experts, k) * (dim + 1) + T * k) * sizeof(float);
 }
 
 extern "C" int fmoe_router_bwd(const float* d_weights, const float* topv, const int32_t* perm,
@@ -324,12 +342,13 @@ extern "C" int fmoe_router_bwd(const float* d_weights, const float* topv, const 
   if (workspace_bytes < fmoe_router_bwd_workspace_bytes(T, dim, n_experts, k))
     return FMOE_ERR_WORKSPACE;
   if (!aligned16(x_perm)) return FMOE_ERR_ALIGN;
-  router_dlogit_kernel<<<dim3(ceil_div(T, 256)), dim3(256), 0, s>>>(d_weights, topv, (int)T, k,
-                                                                    route_scale, d_logits);
   const int64_t max_chunks = router_max_chunks(T, n_experts, k);
   float* partial = static_cast<float*>(workspace);
+  float* dl_row = partial + max_chunks * (dim + 1);
+  router_dlogit_kernel<<<dim3(ceil_div(T * k, 256)), dim3(256), 0, s>>>(
+      d_weights, topv, perm, (int)(T * k), k, route_scale, d_logits, dl_row);
   router_wgrad_partial_kernel<<<dim3(max_chunks), dim3(128), 0, s>>>(
-      d_logits, perm, offsets, n_experts, static_cast<const uint16_t*>(x_perm), (int)dim, partial);
+      dl_row, offsets, n_experts, static_cast<const uint16_t*>(x_perm), (int)dim, partial);
   router_wgrad_final_kernel<<<dim3(ceil_div(dim + 1, 16), n_experts), dim3(256), 0, s>>>(
       partial, offsets, n_experts, (int)dim, grad_dtype, d_gate_w, d_gate_b);
   return launch_status();

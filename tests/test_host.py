@@ -66,7 +66,7 @@ def test_argument_errors_without_gpu():
     # size queries
     assert lib.fmoe_dispatch_workspace_bytes(16384, 8, 2) == 2 * 32 * 8 * 4
     assert lib.fmoe_weight_grad_workspace_bytes(32768, 16384, 8, 768, 2048) > 0
-    assert lib.fmoe_router_bwd_workspace_bytes(16384, 768, 8, 2) == (16384 * 2 // 64 + 8) * 769 * 4
+    assert lib.fmoe_router_bwd_workspace_bytes(16384, 768, 8, 2) == ((16384 * 2 // 32 + 8) * 769 + 16384 * 2) * 4
     assert lib.fmoe_norm_bwd_workspace_bytes(768) == 4160 * 768 * 4
 
 
