@@ -22,7 +22,7 @@ namespace fmoe {
 
 constexpr int kDispThreads = 256;
 constexpr int kDispWaves = kDispThreads / 64;
-constexpr int kSlotsPerThread = 4;
+constexpr int kSlotsPerThread = 1;  // small blocks: 128 of them at T*k = 32768
 constexpr int kSlotsPerBlock = kDispThreads * kSlotsPerThread;
 
 __global__ __launch_bounds__(kDispThreads) void dispatch_hist_kernel(

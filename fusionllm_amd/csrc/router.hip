@@ -26,13 +26,27 @@ constexpr int kRouterMaxDim = 2048;  // a lane keeps its <= 16 x chunks in regis
 // tokens instead of once per token; each lane keeps its x chunks in
 // registers across the expert blocks.  The logits (without bias) go to LDS
 // and every lane of a token's group then computes the scores and the top-k.
+// Lane l gets v from lane l ^ off (off < 16): ds_swizzle in xor mode, within
+// groups of 32 lanes.
+__device__ __forceinline__ float xor_lane(float v, int off) {
+  int r;
+  switch (off) {
+    case 8: r = __builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x001F | (8 << 10)); break;
+    case 4: r = __builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x001F | (4 << 10)); break;
+    case 2: r = __builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x001F | (2 << 10)); break;
+    default: r = __builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x001F | (1 << 10)); break;
+  }
+  return __int_as_float(r);
+}
+
 template <int EB, int NQ>  // NQ: x chunks per lane, NQ * 16 * 8 >= dim
 __global__ __launch_bounds__(512) void router_fwd_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg,
     const uint16_t* __restrict__ bg, int T, int dim, int E, int k, float route_scale,
     int32_t* __restrict__ idx, int64_t* __restrict__ idx64, float* __restrict__ wout,
     float* __restrict__ vout) {
-  __shared__ __attribute__((aligned(16))) uint4 wsh[kRouterEBlk * NQ * kRouterLanes];
+  constexpr int EBLK = EB < kRouterEBlk ? EB : kRouterEBlk;  // experts per LDS block
+  __shared__ __attribute__((aligned(16))) uint4 wsh[EBLK * NQ * kRouterLanes];
   __shared__ float lsh[kRouterTok * EB];
   const int lane16 = threadIdx.x % kRouterLanes;
   const int tl = threadIdx.x / kRouterLanes;
@@ -49,15 +63,15 @@ __global__ __launch_bounds__(512) void router_fwd_kernel(
     xr[q] = c < nchunk ? xrow[c] : make_uint4(0, 0, 0, 0);
   }
 
-  for (int e0 = 0; e0 < E; e0 += kRouterEBlk) {
-    const int ne = min(kRouterEBlk, E - e0);
+  for (int e0 = 0; e0 < E; e0 += EBLK) {
+    const int ne = min(EBLK, E - e0);
     __syncthreads();  // the previous block's gate rows are no longer read
     for (int i = threadIdx.x; i < ne * nchunk; i += blockDim.x)
       wsh[i] = reinterpret_cast<const uint4*>(wg + static_cast<int64_t>(e0) * dim)[i];
     __syncthreads();
-    float acc[kRouterEBlk];
+    float acc[EBLK];
 #pragma unroll
-    for (int e = 0; e < kRouterEBlk; ++e) acc[e] = 0.0f;
+    for (int e = 0; e < EBLK; ++e) acc[e] = 0.0f;
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int c = lane16 + kRouterLanes * q;
@@ -65,7 +79,7 @@ __global__ __launch_bounds__(512) void router_fwd_kernel(
         float xf[8];
         unpack8(xr[q], xf);
 #pragma unroll
-        for (int e = 0; e < kRouterEBlk; ++e) {
+        for (int e = 0; e < EBLK; ++e) {
           if (e < ne) {
             float wf[8];
             unpack8(wsh[e * nchunk + c], wf);
@@ -78,11 +92,11 @@ __global__ __launch_bounds__(512) void router_fwd_kernel(
 #pragma unroll
     for (int off = kRouterLanes / 2; off >= 1; off >>= 1) {
 #pragma unroll
-      for (int e = 0; e < kRouterEBlk; ++e) acc[e] = acc[e] + __shfl_xor(acc[e], off, kRouterLanes);
+      for (int e = 0; e < EBLK; ++e) acc[e] = acc[e] + xor_lane(acc[e], off);
     }
     // every lane now holds the block's logits; lane e writes expert e0 + e
 #pragma unroll
-    for (int e = 0; e < kRouterEBlk; ++e)
+    for (int e = 0; e < EBLK; ++e)
       if (e == lane16 && e < ne) lsh[tl * EB + e0 + e] = acc[e];
   }
   __syncthreads();
@@ -93,38 +107,26 @@ __global__ __launch_bounds__(512) void router_fwd_kernel(
 #pragma unroll
   for (int e = 0; e < EB; ++e) s[e] = (e < E) ? fm_sigmoid(lsh[tl * EB + e] + bf2f(bg[e])) : 0.0f;
 
+  // k selection rounds (a runtime loop over the token's k); lane j keeps the
+  // j-th choice, and the chosen scores are summed in choice order.
   uint64_t taken = 0;
-  int sel[FMOE_MAX_TOPK];
-  float val[FMOE_MAX_TOPK];
+  int e_sel = 0;
+  float v_sel = 0.0f, sum = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    int best = -1;
+    float bv = 0.0f;
 #pragma unroll
-  for (int j = 0; j < FMOE_MAX_TOPK; ++j) {
-    sel[j] = 0;
-    val[j] = 0.0f;
-    if (j < k) {
-      int best = -1;
-      float bv = 0.0f;
-#pragma unroll
-      for (int e = 0; e < EB; ++e) {
-        if (e < E && !((taken >> e) & 1ull)) {
-          if (best < 0 || score_beats(s[e], bv)) { best = e; bv = s[e]; }
-        }
+    for (int e = 0; e < EB; ++e) {
+      if (e < E && !((taken >> e) & 1ull)) {
+        if (best < 0 || score_beats(s[e], bv)) { best = e; bv = s[e]; }
       }
-      taken |= 1ull << best;
-      sel[j] = best;
-      val[j] = bv;
     }
+    taken |= 1ull << best;
+    sum = (j == 0) ? bv : sum + bv;
+    if (j == lane16) { e_sel = best; v_sel = bv; }
   }
-  float sum = val[0];
-#pragma unroll
-  for (int j = 1; j < FMOE_MAX_TOPK; ++j)
-    if (j < k) sum = sum + val[j];
   const float denom = sum + 1e-10f;
   if (active && lane16 < k) {
-    int e_sel = sel[0];
-    float v_sel = val[0];
-#pragma unroll
-    for (int q = 1; q < FMOE_MAX_TOPK; ++q)
-      if (q == lane16) { e_sel = sel[q]; v_sel = val[q]; }
     const int64_t o = static_cast<int64_t>(t) * k + lane16;
     idx[o] = e_sel;
     if (idx64) idx64[o] = e_sel;

@@ -64,7 +64,7 @@ def test_argument_errors_without_gpu():
     assert lib.fmoe_weight_grad(None, None, 8, None, None, 8, None, 1, 10, 0, 128, 128, 0, pp, None, 0,
                                 None, 0, None) == 2
     # size queries
-    assert lib.fmoe_dispatch_workspace_bytes(16384, 8, 2) == 2 * 32 * 8 * 4
+    assert lib.fmoe_dispatch_workspace_bytes(16384, 8, 2) == 2 * 128 * 8 * 4
     assert lib.fmoe_weight_grad_workspace_bytes(32768, 16384, 8, 768, 2048) > 0
     assert lib.fmoe_router_bwd_workspace_bytes(16384, 768, 8, 2) == ((16384 * 2 // 32 + 8) * 769 + 16384 * 2) * 4
     assert lib.fmoe_norm_bwd_workspace_bytes(768) == 4160 * 768 * 4
