@@ -1,5 +1,6 @@
-// gemm.hip — grouped bf16 GEMMs on CDNA4 matrix cores (v_mfma_f32_32x32x16_bf16)
-// for the expert SwiGLU products of FusionLLM's DeepSeekMoE.
+// gemm.hip — grouped bf16 GEMMs on CDNA4 matrix cores
+// (v_mfma_f32_16x16x32_bf16) for the expert SwiGLU products of FusionLLM's
+// DeepSeekMoE.
 //
 // Replaces SwiGLUExpert.forward (models/moe.py:20-21) called once per active
 // expert in the loop of moe.py:66-76 and once for the shared expert
@@ -8,144 +9,30 @@
 // (expert, rows) mapping is computed on the device from offsets[], so no
 // host synchronisation is needed for the ragged, skewed expert sizes.
 //
-// Tiling.  A workgroup computes a BM x BN tile of C with fp32 accumulators,
-// stepping K by 64.  Both operands are staged in LDS as "rows x 64" tiles,
-// K-contiguous (128 bytes per row), double buffered; the 16-byte chunks of a
-// row are XOR-swizzled so that the MFMA fragment reads (32 rows, one chunk)
-// and the transposing stores are free of bank conflicts.  An operand that is
-// MN-contiguous in memory (the weights in the dX products, both operands of
-// the weight gradients) is loaded as 8x8 blocks, transposed in registers and
-// stored K-contiguous.  Each wave owns a WTM x WTN sub-tile made of 32x32
-// MFMA blocks; fragment layout of v_mfma_f32_32x32x16_bf16: lane l supplies
-// A[l%32][8*(l/32) .. +7] and B[8*(l/32) .. +7][l%32] and receives
-// C[8*(r/4) + 4*(l/32) + r%4][l%32] in accumulator r.
+// Row-grouped products (rows_gemm_kernel, modes below): persistent
+// workgroups of 8 waves walk 256 x 256 output tiles in an XCD-contiguous
+// order.  Both operands are K-contiguous in memory and reach LDS through
+// global_load_lds copies (no registers) into a two-stage ring of 64-deep K
+// steps that runs on across tile boundaries; a wave owns a 64 x 128 block
+// and runs the hand-scheduled K step of gemm_core.h.  The epilogue stages
+// each 16-row slice through LDS for 16-byte stores and fuses the SwiGLU
+// (forward: a | b and h = silu(a) * b; backward: da, db from dh, a, b).  The
+// tiles of the last, partial round of the plain-output products are split
+// along K, with fp32 partials summed in range order by split_reduce_kernel.
+//
+// Weight gradients (wgrad_tr_kernel): work units (group, K chunk, tile);
+// both operands are MN-contiguous, copied as they lie and read with
+// ds_read_b64_tr_b16 (transposing LDS reads); multi-chunk groups write fp32
+// partials that wgrad_reduce_kernel adds in chunk order.
+//
+// Decode-sized launches send groups of at most kSmallM rows to
+// small_gemm_kernel, which streams the weights once.
 #include <atomic>
 
 #include "fmoe_common.h"
 #include "gemm_core.h"
 
 namespace fmoe {
-
-constexpr int kBK = 64;
-
-__device__ __forceinline__ uint32_t lds_off(int row, int chunk) {
-  return static_cast<uint32_t>(row) * 128u +
-         (static_cast<uint32_t>(chunk ^ ((row ^ (row >> 3)) & 7)) << 4);
-}
-
-template <int BM_, int BN_, int WAVES_M_, int WAVES_N_>
-struct Cfg {
-  static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
-  static constexpr int NT = WAVES_M * WAVES_N * 64;
-  static constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
-  static constexpr int FM = WTM / 32, FN = WTN / 32;
-  static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
-  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
-  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be made of 32x32 blocks");
-};
-
-// ---- operand staging --------------------------------------------------------
-// K-contiguous operand: ROWS rows x 64 k.  Thread t moves chunk t%8 of rows
-// t/8, t/8 + NT/8, ...
-template <int ROWS, int NT>
-struct KLoad {
-  static constexpr int PER = ROWS * 8 / NT;
-  static_assert(PER >= 1 && (ROWS * 8) % NT == 0, "K-major tile does not split evenly");
-  const uint16_t* src[PER];
-  uint4 reg[PER];
-  __device__ __forceinline__ static int row_of(int tid, int i) { return (tid >> 3) + i * (NT / 8); }
-  __device__ __forceinline__ static int chunk_of(int tid) { return tid & 7; }
-  __device__ __forceinline__ void load(int k0) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) reg[i] = *reinterpret_cast<const uint4*>(src[i] + k0);
-  }
-  __device__ __forceinline__ void store(uint8_t* s, int tid) const {
-#pragma unroll
-    for (int i = 0; i < PER; ++i)
-      *reinterpret_cast<uint4*>(s + lds_off(row_of(tid, i), chunk_of(tid))) = reg[i];
-  }
-};
-
-// MN-contiguous operand: memory is [k][mn]; the tile is ROWS mn x 64 k.  Work
-// item b = (mn block mb = b % (ROWS/8), k block kb = b / (ROWS/8)) moves an
-// 8 (k) x 8 (mn) block: 8 row loads of 16 bytes, an in-register transpose,
-// 8 stores of 16 bytes into LDS rows mb*8 .. mb*8+7 at chunk kb.  NTL threads
-// take part, numbered by the caller (ltid outside [0, NTL) does nothing), so
-// that two operands can be split over the two halves of a workgroup.
-template <int ROWS, int NTL>
-struct MNLoad {
-  static constexpr int NBLK = ROWS;  // (ROWS / 8) * (64 / 8)
-  static constexpr int PER = NBLK / NTL;
-  static_assert(NBLK % NTL == 0 && PER >= 1, "MN-major tile split");
-  uint4 reg[PER][8];
-  __device__ __forceinline__ static bool active(int ltid) { return ltid >= 0 && ltid < NTL; }
-  __device__ __forceinline__ static int blk(int ltid, int p) { return ltid + p * NTL; }
-  __device__ __forceinline__ static int mb_of(int b) { return b % (ROWS / 8); }
-  __device__ __forceinline__ static int kb_of(int b) { return b / (ROWS / 8); }
-
-  // rowptr(k) -> pointer to element (k, 0) of the operand, nullptr for a row
-  // that lies outside the reduction range (loaded as zeros).  Columns are
-  // clamped to [0, mn_limit - 8]: a clamped block only feeds outputs that the
-  // epilogue does not store.
-  template <class RowPtr>
-  __device__ __forceinline__ void load(int ltid, int k0, int mn0, int mn_limit, RowPtr rowptr) {
-    if (!active(ltid)) return;
-#pragma unroll
-    for (int p = 0; p < PER; ++p) {
-      const int b = blk(ltid, p);
-      int col = mn0 + mb_of(b) * 8;
-      col = col < mn_limit - 8 ? col : mn_limit - 8;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint16_t* r = rowptr(k0 + kb_of(b) * 8 + i);
-        if (r) reg[p][i] = *reinterpret_cast<const uint4*>(r + col);
-        else reg[p][i] = make_uint4(0, 0, 0, 0);
-      }
-    }
-  }
-  __device__ __forceinline__ void store(uint8_t* s, int ltid) const {
-    if (!active(ltid)) return;
-#pragma unroll
-    for (int p = 0; p < PER; ++p) {
-      const int b = blk(ltid, p);
-      const uint32_t* in = reinterpret_cast<const uint32_t*>(&reg[p][0]);  // in[4*i + dword]
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        uint32_t o[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t lo = in[4 * (2 * q) + (j >> 1)];
-          const uint32_t hi = in[4 * (2 * q + 1) + (j >> 1)];
-          o[q] = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-        }
-        *reinterpret_cast<uint4*>(s + lds_off(mb_of(b) * 8 + j, kb_of(b))) =
-            make_uint4(o[0], o[1], o[2], o[3]);
-      }
-    }
-  }
-};
-
-// One K-tile (64) of MFMAs from the staged A and B tiles.
-template <class C>
-__device__ __forceinline__ void mma_ktile(const uint8_t* sA, const uint8_t* sB,
-                                          f32x16 (&acc)[C::FM][C::FN], int wm, int wn, int lane) {
-#pragma unroll
-  for (int kk = 0; kk < kBK / 16; ++kk) {
-    const int chunk = kk * 2 + (lane >> 5);
-    bf16x8 a[C::FM], b[C::FN];
-#pragma unroll
-    for (int fm = 0; fm < C::FM; ++fm)
-      a[fm] = *reinterpret_cast<const bf16x8*>(sA + lds_off(wm * C::WTM + fm * 32 + (lane & 31), chunk));
-#pragma unroll
-    for (int fn = 0; fn < C::FN; ++fn)
-      b[fn] = *reinterpret_cast<const bf16x8*>(sB + lds_off(wn * C::WTN + fn * 32 + (lane & 31), chunk));
-#pragma unroll
-    for (int fm = 0; fm < C::FM; ++fm)
-#pragma unroll
-      for (int fn = 0; fn < C::FN; ++fn)
-        acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[fm], b[fn], acc[fm][fn], 0, 0, 0);
-  }
-}
 
 // ---- row-grouped products ---------------------------------------------------
 // Every row-grouped product streams both operands K-contiguous: the
@@ -765,102 +652,6 @@ __device__ __forceinline__ void store_grad(const WgradArgs& a, int g, int m, int
   else static_cast<float*>(base)[o] = v;
 }
 
-template <class C>
-__global__ __launch_bounds__(C::NT) void wgrad_kernel(const WgradArgs args) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::STAGE_BYTES];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
-  const int tiles_m = (args.m_out + C::BM - 1) / C::BM;
-  const int tiles_n = (args.n_out + C::BN - 1) / C::BN;
-  const int tiles = tiles_m * tiles_n;
-  const int G = args.E + (args.rows_shared > 0 ? 1 : 0);
-
-  int unit = blockIdx.x;
-  int g = 0, row_base = 0, M = 0, chunks = 0, pbase = 0;
-  for (; g < G; ++g) {
-    group_rows(args, g, row_base, M);
-    chunks = (M + args.kc - 1) / args.kc;
-    const int nu = chunks * tiles;
-    if (unit < nu) break;
-    unit -= nu;
-    if (chunks > 1) pbase += chunks;
-  }
-  if (g >= G) return;
-  const int chunk = unit / tiles, tile = unit % tiles;
-  const int tm = tile / tiles_n, tn = tile % tiles_n;
-  const int m0 = tm * C::BM, n0 = tn * C::BN;
-  const int k_begin = chunk * args.kc;
-  const int k_end = min(M, k_begin + args.kc);
-
-  const bool shared_sep = (g >= args.E);
-  const uint16_t* A = (shared_sep && args.a_shared) ? args.a_shared
-                                                   : args.a_routed + static_cast<int64_t>(row_base) * args.lda;
-  const uint16_t* B = (shared_sep && args.b_shared) ? args.b_shared
-                                                   : args.b_routed + static_cast<int64_t>(row_base) * args.ldb;
-  auto a_row = [&](int k) -> const uint16_t* {
-    return k < k_end ? A + static_cast<int64_t>(k) * args.lda : nullptr;
-  };
-  auto b_row = [&](int k) -> const uint16_t* {
-    return k < k_end ? B + static_cast<int64_t>(k) * args.ldb : nullptr;
-  };
-  // With 512 threads the A blocks go to threads 0-255 and the B blocks to
-  // threads 256-511; with 256 threads every thread moves one block of each.
-  constexpr int NTL = C::NT >= 512 ? C::NT / 2 : C::NT;
-  MNLoad<C::BM, NTL> la;
-  MNLoad<C::BN, NTL> lb;
-  const int a_ltid = tid;
-  const int b_ltid = C::NT >= 512 ? tid - NTL : tid;
-  auto load_tile = [&](int k0) {
-    la.load(a_ltid, k0, m0, args.m_out, a_row);
-    lb.load(b_ltid, k0, n0, args.n_out, b_row);
-  };
-  auto store_tile = [&](int buf) {
-    uint8_t* sA = smem + buf * C::STAGE_BYTES;
-    la.store(sA, a_ltid);
-    lb.store(sA + C::A_BYTES, b_ltid);
-  };
-
-  f32x16 acc[C::FM][C::FN];
-#pragma unroll
-  for (int fm = 0; fm < C::FM; ++fm)
-#pragma unroll
-    for (int fn = 0; fn < C::FN; ++fn)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
-
-  const int nk = (k_end - k_begin + kBK - 1) / kBK;
-  load_tile(k_begin);
-  store_tile(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) load_tile(k_begin + (kt + 1) * kBK);
-    const uint8_t* sA = smem + buf * C::STAGE_BYTES;
-    mma_ktile<C>(sA, sA + C::A_BYTES, acc, wm, wn, lane);
-    if (kt + 1 < nk) store_tile(buf ^ 1);
-    __syncthreads();
-  }
-
-  const int row_l = (lane >> 5) * 4;
-  const int64_t mn = static_cast<int64_t>(args.m_out) * args.n_out;
-  float* part = (chunks > 1) ? args.partial + static_cast<int64_t>(pbase + chunk) * mn : nullptr;
-#pragma unroll
-  for (int fm = 0; fm < C::FM; ++fm) {
-#pragma unroll
-    for (int fn = 0; fn < C::FN; ++fn) {
-      const int n = n0 + wn * C::WTN + fn * 32 + (lane & 31);
-      if (n >= args.n_out) continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * C::WTM + fm * 32 + (r >> 2) * 8 + row_l + (r & 3);
-        if (m >= args.m_out) continue;
-        if (part) part[static_cast<int64_t>(m) * args.n_out + n] = acc[fm][fn][r];
-        else store_grad(args, g, m, n, acc[fm][fn][r]);
-      }
-    }
-  }
-}
-
 // ---- weight gradients on the shared core ------------------------------------
 // Both operands are MN-contiguous ([rows, m_out] and [rows, n_out]), so their
 // 64 x 256 stage tiles are copied as they lie in memory (K-major: 64 k rows of
@@ -1098,8 +889,6 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const WgradArgs args)
 }
 
 // ---- host side --------------------------------------------------------------
-using CfgWgrad = Cfg<256, 256, 2, 4>;
-
 int check_common(int n_experts, int64_t rows_routed, int64_t rows_shared, int64_t dim, int64_t inter) {
   if (n_experts <= 0 || n_experts > FMOE_MAX_EXPERTS) return FMOE_ERR_TOO_MANY_EXPERTS;
   if (rows_routed < 0 || rows_shared < 0 || dim <= 0 || inter <= 0) return FMOE_ERR_INVALID_ARG;
