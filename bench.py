@@ -49,6 +49,9 @@ def parse():
     p.add_argument("--cpu-tokens", type=int, default=2048, help="token sample for the CPU baseline")
     p.add_argument("--fwd-only", action="store_true",
                    help="time the forward pass alone (decode-shaped C3 configs); not the headline metric")
+    p.add_argument("--optimizer", action="store_true",
+                   help="time the fused NorMuon step on the block's weight matrices (fp32, as the trainer "
+                        "keeps them) instead of the block; its own JSON line")
     p.add_argument("--copy-calibration", action="store_true",
                    help="run only a device-to-device copy of COPY_BYTES (3 times): the known-size kernel whose "
                         "FETCH_SIZE / WRITE_SIZE counters scale the GEMM counters to HBM bytes")
@@ -169,10 +172,89 @@ def cpu_baseline(cfg, data, n_tokens):
     }
 
 
+def optimizer_bench(args):
+    """NorMuon step (training/optimizer.py:11-58) over the weight matrices of
+    the workload's MoE block (what build_optimizers gives NorMuon there: the
+    expert and shared-expert matrices and gate.weight), fp32 parameters and
+    states as the trainer keeps them, synthetic gradients."""
+    from fusionllm_amd import DeepSeekMoE, configs
+    from fusionllm_amd.optim import NorMuon
+    from fusionllm_amd import _kernels as K
+    cfg = configs.ALL.get(args.config) or next(c for n, c in configs.ALL.items() if n.split("-")[0] == args.config)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    m = DeepSeekMoE(cfg.moe_config()).to(dev)
+    mats = [p for p in m.parameters() if p.ndim >= 2]
+    g = torch.Generator(device=dev).manual_seed(0)
+    for p in mats:
+        p.grad = torch.randn(p.shape, generator=g, device=dev) * 1e-3
+    opt = NorMuon(mats, lr=0.02, betas=(0.95, 0.95))
+    for _ in range(args.warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    timer = {}
+    K.set_timer(timer, only={"normuon_step"})
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        opt.step()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    K.set_timer(None)
+    elapsed = max(start.elapsed_time(end) / 1e3, wall)
+    n_el = sum(p.numel() for p in mats)
+    launches = [a.elapsed_time(b) / 1e3 for a, b in timer["normuon_step"]]
+    per_launch = sum(launches) / len(launches)
+    launches_per_step = len(launches) // args.steps
+    bytes_per_el = 7 * 4  # read p, grad, exp_avg, exp_avg_sq; write p, exp_avg, exp_avg_sq (fp32)
+    work = n_el * bytes_per_el / launches_per_step
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import moe_oracle as mo
+        torch.set_num_threads(os.cpu_count() or 1)
+        sample = [p.detach().cpu().clone() for p in mats[:3]]
+        grads = [p.grad.cpu() for p in mats[:3]]
+        states = [{} for _ in sample]
+        for q, gq, st in zip(sample, grads, states):  # warmup (state allocation)
+            mo.normuon_step(q, gq, st, lr=0.02, betas=(0.95, 0.95))
+        times = []
+        for _ in range(3):
+            c0 = time.perf_counter()
+            for q, gq, st in zip(sample, grads, states):
+                mo.normuon_step(q, gq, st, lr=0.02, betas=(0.95, 0.95))
+            times.append(time.perf_counter() - c0)
+        n_s = sum(q.numel() for q in sample)
+        cpu = {"value": round(n_s / statistics.median(times), 1), "unit": "elements/s",
+               "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"3 of the {len(mats)} matrices ({n_s} elements), the reference's step op by op in torch "
+                         f"CPU, fp32, median of 3 after 1 warmup"}
+    line = {
+        "metric": "NorMuon step elements/sec (fp32 weight matrices of the MoE block)",
+        "value": round(n_el * args.steps / elapsed, 1),
+        "unit": "elements/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (N(0, 1e-3^2) gradients; module init weights)",
+        "config": {"workload": f"NorMuon on {cfg.name} block matrices", "tensors": len(mats), "elements": n_el},
+        "roofline": {"kernel": "normuon_step", "bound": "hbm", "achieved": round(work / per_launch / 1e9, 1),
+                     "peak": PEAK_HBM_BYTES / 1e9, "unit": "GB/s",
+                     "frac": round(work / per_launch / PEAK_HBM_BYTES, 4), "traffic": None,
+                     "work_per_launch": work, "launches_timed": len(launches)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.optimizer:
+        optimizer_bench(args)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only (one MI355X per box); "

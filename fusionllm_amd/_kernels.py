@@ -334,3 +334,38 @@ def dx_reduce_norm(dx_rows, pos, idx, d_logits, gate_w, rows_routed: int, has_sh
                                   ws_bytes, _stream()),
           "fmoe_dx_reduce_norm")
     return dx, dnw
+
+
+NORMUON_MAX_TENSORS = 32
+
+
+@_timed
+def normuon_step(params, grads, exp_avgs, exp_avg_sqs, lr: float, beta1: float, beta2: float, eps: float,
+                 weight_decay: float, cautious: bool, bias_corr1: float, bias_corr2: float):
+    """One fused NorMuon update of up to 32 same-dtype tensors (in place)."""
+    lib = _lib.load()
+    n = len(params)
+    if n > NORMUON_MAX_TENSORS:
+        raise RuntimeError(f"at most {NORMUON_MAX_TENSORS} tensors per launch (got {n})")
+    dt = params[0].dtype
+    rows = (ctypes.c_int64 * n)()
+    cols = (ctypes.c_int64 * n)()
+    mat = (ctypes.c_int * n)()
+    ptrs = [[], [], [], []]
+    for i, (p, g, m, v) in enumerate(zip(params, grads, exp_avgs, exp_avg_sqs)):
+        for t, name in ((p, "param"), (g, "grad"), (m, "exp_avg"), (v, "exp_avg_sq")):
+            _req(t, name, dt)
+            if t.shape != p.shape:
+                raise RuntimeError(f"{name} shape {tuple(t.shape)} != param shape {tuple(p.shape)}")
+        c = p.shape[-1] if p.dim() >= 1 else 1
+        rows[i] = p.numel() // c if c else 0
+        cols[i] = c
+        mat[i] = 1 if p.dim() >= 2 else 0
+        for lst, t in zip(ptrs, (p, g, m, v)):
+            lst.append(t.data_ptr())
+    # ptr_array caches by content: these arrays change every call, build them fresh
+    arrs = [(ctypes.c_void_p * n)(*lst) for lst in ptrs]
+    check(lib.fmoe_normuon_step(arrs[0], arrs[1], arrs[2], arrs[3], rows, cols, mat, n, _dtype_code(dt),
+                                float(lr), float(beta1), float(beta2), float(eps), float(weight_decay),
+                                int(bool(cautious)), float(bias_corr1), float(bias_corr2), _stream()),
+          "fmoe_normuon_step")

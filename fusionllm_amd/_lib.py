@@ -9,11 +9,11 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
-from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_size_t, c_void_p
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libfusionmoe.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 MAX_EXPERTS = 64
 MAX_TOPK = 8
 
@@ -60,6 +60,9 @@ SIGNATURES = {
     "fmoe_norm_bwd_workspace_bytes": (c_size_t, [c_int64]),
     "fmoe_dx_reduce_norm": (c_int, [_P, _P, _P, _P, _P, c_int64, c_int64, c_int, c_int64, c_int,
                                     _P, _P, _P, c_int, _P, c_int, _P, _P, _P, c_size_t, _P]),
+    "fmoe_normuon_step": (c_int, [_PP, _PP, _PP, _PP, POINTER(c_int64), POINTER(c_int64), POINTER(c_int),
+                                  c_int, c_int, c_double, c_double, c_double, c_double, c_double, c_int,
+                                  c_double, c_double, _P]),
 }
 
 _lock = threading.Lock()

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define FMOE_ABI_VERSION 4
+#define FMOE_ABI_VERSION 5
 #define FMOE_MAX_EXPERTS 64
 #define FMOE_MAX_TOPK 8
 
@@ -277,6 +277,26 @@ int fmoe_dx_reduce_norm(const void* dx_rows, const int32_t* pos_of_slot,
                         int w_dtype, const void* d_out, int x_dtype, void* dx,
                         void* d_norm_w, void* workspace, size_t workspace_bytes,
                         void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused NorMuon step (training/optimizer.py:11-58, NorMuon.step) for up to 32
+ * tensors of one dtype and one step count: exp_avg, exp_avg_sq and the
+ * parameter are updated in place, with the reference's operation order and
+ * per-operation rounding to the tensor dtype (fp32 arithmetic).  Tensor i is
+ * rows[i] x cols[i] (row-major, cols % 4 == 0, cols <= 4096); is_matrix[i]
+ * (the parameter has ndim >= 2) enables the per-row RMS normalisation and the
+ * cautious weight decay.  The scalars are the reference's Python values:
+ * bias_corr1 = 1 - beta1**step, bias_corr2 = 1 - beta2**step.  Host arrays;
+ * grads are read-only.  Deterministic (one wave per row, fixed-order row
+ * sums).
+ * ------------------------------------------------------------------------- */
+int fmoe_normuon_step(void* const* params, const void* const* grads,
+                      void* const* exp_avgs, void* const* exp_avg_sqs,
+                      const int64_t* rows, const int64_t* cols,
+                      const int* is_matrix, int n_tensors, int dtype,
+                      double lr, double beta1, double beta2, double eps,
+                      double weight_decay, int cautious, double bias_corr1,
+                      double bias_corr2, void* stream);
 
 #ifdef __cplusplus
 }

@@ -14,6 +14,7 @@ Every function follows the reference op by op, in the reference's dtypes:
   block_forward   fusionllm.py:50-53 (ffn half) x + moe(RMSNorm(x)), eps 1e-6
   gate_bias_step  moe.py:89-98   bincount, 1.10/0.90 x mean thresholds, masked +-speed
   load_balance_loss moe.py:100-109 E * sum(f * P) with one-hot P
+  normuon_step    training/optimizer.py:18-58 NorMuon.step on one parameter
 Router modes:
   "module" — the reference exactly: logits and scores in the module dtype,
              torch.topk (its own tie order);
@@ -156,6 +157,76 @@ def load_balance_loss(indices, weights, n_experts: int):
     onehot = F.one_hot(flat, num_classes=n_experts).float()
     prob = (onehot * weights.flatten().unsqueeze(-1)).view(T, k, n_experts).sum(dim=1).mean(dim=0)
     return (frac * prob).sum() * n_experts
+
+
+@torch.no_grad()
+def normuon_step(p, grad, state: dict, lr: float = 0.02, betas=(0.9, 0.95), eps: float = 1e-8,
+                 weight_decay: float = 0.1, cautious_wd: bool = True):
+    """NorMuon.step for one parameter, training/optimizer.py:18-58, op by op;
+    updates p and state in place.
+
+    fp32: the reference's tensor operations as written.  bf16: the same
+    operations as torch runs them on the GPU (where the reference trains):
+    fp32 arithmetic with the Python scalars in fp32, each result rounded to
+    bf16, "a + s*b" as one fused multiply-add.  (torch's CPU kernels instead
+    round the alpha/value scalars of add_/addcmul_ to bf16, which changes
+    about a fifth of the first step's exp_avg elements.)
+    """
+    beta1, beta2 = betas
+    if len(state) == 0:
+        state["step"] = 0
+        state["exp_avg"] = torch.zeros_like(grad)
+        state["exp_avg_sq"] = torch.zeros_like(grad)
+    exp_avg, exp_avg_sq = state["exp_avg"], state["exp_avg_sq"]
+    state["step"] += 1
+    step_count = state["step"]
+    bias_corr1 = 1.0 - beta1 ** step_count
+    bias_corr2 = 1.0 - beta2 ** step_count
+    if p.dtype == torch.bfloat16:
+        _normuon_bf16(p, grad, exp_avg, exp_avg_sq, lr, beta1, beta2, eps, weight_decay, cautious_wd,
+                      bias_corr1, bias_corr2)
+        return
+    exp_avg.mul_(beta1).add_(grad, alpha=1.0 - beta1)
+    exp_avg_sq.mul_(beta2).addcmul_(grad, grad, value=1.0 - beta2)
+    denom = (exp_avg_sq.sqrt() / (bias_corr2 ** 0.5)).add_(eps)
+    update = exp_avg / bias_corr1 / denom
+    if p.ndim >= 2:
+        row_norm = update.norm(p=2, dim=-1, keepdim=True)
+        row_rms = row_norm / (update.size(-1) ** 0.5 + eps)
+        update = update / (row_rms + eps)
+    if weight_decay > 0:
+        if cautious_wd and p.ndim >= 2:
+            mask = (grad * p).sign() == 1.0
+            p.mul_(1.0 - lr * weight_decay * mask.to(p.dtype))
+        else:
+            p.mul_(1.0 - lr * weight_decay)
+    p.add_(update, alpha=-lr)
+
+
+def _normuon_bf16(p, grad, exp_avg, exp_avg_sq, lr, beta1, beta2, eps, weight_decay, cautious_wd,
+                  bias_corr1, bias_corr2):
+    f32 = lambda v: torch.tensor(v, dtype=torch.float32)  # a Python scalar as the GPU kernels see it
+    r = lambda t: t.to(torch.bfloat16).float()             # round an operation's result to bf16
+    fma = lambda a, b, c: (a.double() * b.double() + c.double()).float()
+    g, w = grad.float(), p.float()
+    m = r(fma(f32(1.0 - beta1), g, r(exp_avg.float() * f32(beta1))))
+    v = r(fma(f32(1.0 - beta2) * g, g, r(exp_avg_sq.float() * f32(beta2))))
+    denom = r(r(r(v.sqrt()) / f32(bias_corr2 ** 0.5)) + f32(eps))
+    update = r(r(m / f32(bias_corr1)) / denom)
+    if p.ndim >= 2:
+        row_norm = r(update.double().pow(2).sum(-1, keepdim=True).sqrt().float())
+        row_rms = r(row_norm / f32(update.size(-1) ** 0.5 + eps))
+        update = r(update / r(row_rms + f32(eps)))
+    if weight_decay > 0:
+        if cautious_wd and p.ndim >= 2:
+            mask = (r(g * w) > 0).float()
+            w = r(w * r(1.0 - r(f32(lr * weight_decay) * mask)))
+        else:
+            w = r(w * f32(1.0 - lr * weight_decay))
+    w = r(fma(f32(-lr), update, w))
+    exp_avg.copy_(m)
+    exp_avg_sq.copy_(v)
+    p.copy_(w)
 
 
 # ---- C restatement wrappers -------------------------------------------------------

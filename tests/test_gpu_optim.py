@@ -1,0 +1,124 @@
+"""Parity of the fused NorMuon step (training/optimizer.py:11-58) on the GPU.
+
+Reference: oracle.moe_oracle.normuon_step, the reference's step restated op
+by op in torch on the CPU, in the parameter's dtype, on the same inputs.
+
+Tolerances (stated here, applied below), after 3 steps:
+  fp32   parameter, exp_avg, exp_avg_sq: |d| <= 4e-6 |x| + 1e-5 rms(x).  Both
+         paths round every operation to fp32; they differ in the fused
+         multiply-adds of add_/addcmul_ and in the order of the row sum of
+         squares: a few ulps of the O(1) update, i.e. about 1e-8 absolute
+         after lr = 0.02, which near-zero parameters see as relative error
+         (hence the floor, 2e-7 for the 0.02-scale parameters here).
+  bf16   |d| <= 1 ulp(x) + atol and >= 99.9 % of the elements bit-equal.
+         The oracle runs the reference's operations with the GPU's scalar
+         handling (fp32 scalars, each result rounded to bf16); the paths
+         differ only where a fused multiply-add rounds twice (fp32, then
+         bf16) and in the order of the row sum of squares.  A last-bit
+         difference in the update u (O(1) after the row normalisation) moves
+         the parameter by lr * 2^-8 per step (atol = steps * lr * 2^-8 for
+         the parameter, 1e-3 rms(x) for the moments near zero).
+"""
+import pytest
+import torch
+
+from fusionllm_amd import DeepSeekMoE, configs
+from fusionllm_amd.optim import NorMuon
+from oracle import moe_oracle as mo
+
+pytestmark = pytest.mark.gpu
+
+
+def _ulps(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    def key(t):
+        i = t.contiguous().view(torch.int16).to(torch.int32)
+        return torch.where(i < 0, -(i & 0x7FFF), i)
+    return (key(a) - key(b)).abs()
+
+
+def _bf16_ulp(t: torch.Tensor) -> torch.Tensor:
+    m = t.double().abs().clamp_min(2.0 ** -126)
+    return torch.exp2(torch.floor(torch.log2(m)) - 7)
+
+
+def _compare(got: torch.Tensor, want: torch.Tensor, what: str, update_atol: float = 0.0):
+    got = got.detach().cpu()
+    w64 = want.double()
+    err = (got.double() - w64).abs()
+    rms = w64.pow(2).mean().sqrt()
+    if want.dtype == torch.float32:
+        bad = err > 4e-6 * w64.abs() + 1e-5 * rms
+    else:
+        bad = err > _bf16_ulp(w64) + max(1e-3 * float(rms), update_atol)
+        assert float((_ulps(got, want) == 0).double().mean()) >= 0.999, what
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements beyond tolerance, max err {float(err.max()):.3e}"
+
+
+SHAPES = [(2048, 768), (768, 2048), (37, 12), (100, 64), (768,)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("wd,cautious", [(0.1, True), (0.1, False), (0.0, True)])
+def test_normuon_matches_reference_step(gpu_device, dtype, wd, cautious):
+    g = torch.Generator().manual_seed(7)
+    ps = [(torch.randn(*s, generator=g) * 0.02).to(dtype) for s in SHAPES]
+    grads = [[(torch.randn(*s, generator=g) * 1e-3).to(dtype) for s in SHAPES] for _ in range(3)]
+    ref_p = [p.clone() for p in ps]
+    ref_st = [{} for _ in ps]
+    dev_p = [torch.nn.Parameter(p.to(gpu_device)) for p in ps]
+    opt = NorMuon(dev_p, lr=0.02, betas=(0.95, 0.95), eps=1e-8, weight_decay=wd, cautious_wd=cautious)
+    for step in range(3):
+        for i in range(len(ps)):
+            mo.normuon_step(ref_p[i], grads[step][i], ref_st[i], lr=0.02, betas=(0.95, 0.95), eps=1e-8,
+                            weight_decay=wd, cautious_wd=cautious)
+            dev_p[i].grad = grads[step][i].to(gpu_device)
+        opt.step()
+    for i, s in enumerate(SHAPES):
+        st = opt.state[dev_p[i]]
+        assert st["step"] == 3
+        _compare(dev_p[i], ref_p[i], f"param {s}", update_atol=3 * 0.02 * 2.0 ** -8)
+        _compare(st["exp_avg"], ref_st[i]["exp_avg"], f"exp_avg {s}")
+        _compare(st["exp_avg_sq"], ref_st[i]["exp_avg_sq"], f"exp_avg_sq {s}")
+
+
+def test_normuon_many_tensors_and_mixed_steps(gpu_device):
+    # 40 tensors (two launches of at most 32) and one parameter that joins a
+    # step later (its own step count, its own launch).
+    g = torch.Generator().manual_seed(3)
+    ps = [torch.nn.Parameter((torch.randn(8, 16, generator=g) * 0.1).to(gpu_device)) for _ in range(40)]
+    late = torch.nn.Parameter((torch.randn(4, 8, generator=g) * 0.1).to(gpu_device))
+    opt = NorMuon(ps + [late], lr=0.01)
+    ref = [p.detach().cpu().clone() for p in ps] + [late.detach().cpu().clone()]
+    ref_st = [{} for _ in ref]
+    for step in range(2):
+        for i, p in enumerate(ps + [late]):
+            if p is late and step == 0:
+                p.grad = None
+                continue
+            gr = torch.randn(p.shape, generator=g) * 1e-2
+            p.grad = gr.to(gpu_device)
+            mo.normuon_step(ref[i], gr, ref_st[i], lr=0.01)
+        opt.step()
+    assert opt.state[late]["step"] == 1 and opt.state[ps[0]]["step"] == 2
+    for i, p in enumerate(ps + [late]):
+        _compare(p, ref[i], f"tensor {i}")
+
+
+def test_normuon_on_expert_weights_after_backward(gpu_device):
+    # The optimizer on the MoE block's expert matrices (the parameters the
+    # reference's build_optimizers gives NorMuon, training/optimizer.py:113-152),
+    # fp32 module under bf16 autocast as the trainer runs it.
+    cfg = configs.BlockConfig("opt", 512, dim=256, inter=512, n_experts=4, topk=2, bias="skew")
+    data = configs.make_block(cfg, seed=11)
+    m = DeepSeekMoE(cfg.moe_config())
+    m.load_state_dict(data.state_dict())
+    m = m.to(gpu_device)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = m(data.x.to(gpu_device))
+    y.float().pow(2).mean().backward()
+    mats = [p for n, p in m.named_parameters() if p.ndim >= 2 and p.grad is not None]
+    ref = [(p.detach().cpu().clone(), p.grad.detach().cpu().clone()) for p in mats]
+    NorMuon(mats, lr=0.02, betas=(0.95, 0.95)).step()
+    for (p0, g0), p in zip(ref, mats):
+        mo.normuon_step(p0, g0, {}, lr=0.02, betas=(0.95, 0.95))
+        _compare(p, p0, "expert matrix")

@@ -21,7 +21,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     syms = declared_symbols()
-    assert len(syms) == 21
+    assert len(syms) == 22
     for s in syms:
         assert hasattr(lib, s), s
     assert set(syms) == set(_lib.SIGNATURES), "ctypes binding and header disagree"
@@ -68,6 +68,16 @@ def test_argument_errors_without_gpu():
     assert lib.fmoe_weight_grad_workspace_bytes(32768, 16384, 8, 768, 2048) > 0
     assert lib.fmoe_router_bwd_workspace_bytes(16384, 768, 8, 2) == ((16384 * 2 // 32 + 8) * 769 + 16384 * 2) * 4
     assert lib.fmoe_norm_bwd_workspace_bytes(768) == 4160 * 768 * 4
+    # fused NorMuon step: limits checked before any pointer is used
+    import ctypes
+    pp1 = _lib.ptr_array([1 << 20])
+    r1, c1, m1 = (ctypes.c_int64 * 1)(4), (ctypes.c_int64 * 1)(6), (ctypes.c_int * 1)(1)
+    assert lib.fmoe_normuon_step(pp1, pp1, pp1, pp1, r1, c1, m1, 33, 0, .02, .9, .95, 1e-8, .1, 1, .1, .05,
+                                 None) == 1  # more than 32 tensors
+    assert lib.fmoe_normuon_step(pp1, pp1, pp1, pp1, r1, c1, m1, 1, 7, .02, .9, .95, 1e-8, .1, 1, .1, .05,
+                                 None) == 4  # dtype
+    assert lib.fmoe_normuon_step(pp1, pp1, pp1, pp1, r1, c1, m1, 1, 0, .02, .9, .95, 1e-8, .1, 1, .1, .05,
+                                 None) == 2  # cols not a multiple of 4
 
 
 def test_parameter_names_shapes_and_count():

@@ -266,3 +266,50 @@ def test_rms_norm_is_torch_rms_norm_and_planted_mistakes_fail():
     xb[0] = 1e-4
     ref = mo.rms_norm(xb, wb, 1e-6)
     assert ulps(mo.rms_norm(xb, wb, 0.0)[0], ref[0]) > 1
+
+
+def test_normuon_oracle_closed_forms():
+    # training/optimizer.py:18-58.  Constant gradient g from zero state: the
+    # bias-corrected moments are g and g^2 at every step, so the update is
+    # u = g / (|g| + eps) (then each matrix row divided by its RMS + eps), and
+    # with wd = 0 the parameter moves by -lr * u per step.
+    g64 = torch.Generator().manual_seed(1)
+    p0 = torch.randn(6, 8, generator=g64, dtype=torch.float64)
+    g = torch.randn(6, 8, generator=g64, dtype=torch.float64)
+    p, st = p0.clone(), {}
+    for t in range(1, 4):
+        mo.normuon_step(p, g, st, lr=0.01, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.0)
+        u = g / (g.abs() + 1e-8)
+        rms = u.norm(dim=-1, keepdim=True) / (8 ** 0.5 + 1e-8)
+        u = u / (rms + 1e-8)
+        assert torch.allclose(p, p0 - 0.01 * t * u, rtol=0, atol=1e-12)
+        assert st["step"] == t
+        assert torch.allclose(st["exp_avg"], (1 - 0.9 ** t) * g, rtol=1e-12, atol=0)
+    # a vector: no row normalisation, plain (not cautious) decay
+    v0 = torch.randn(8, generator=g64, dtype=torch.float64)
+    gv = torch.randn(8, generator=g64, dtype=torch.float64)
+    v, st = v0.clone(), {}
+    mo.normuon_step(v, gv, st, lr=0.01, eps=1e-8, weight_decay=0.1)
+    assert torch.allclose(v, v0 * (1 - 0.001) - 0.01 * gv / (gv.abs() + 1e-8), rtol=0, atol=1e-12)
+    # cautious decay: only where grad * param > 0
+    q0 = torch.tensor([[1.0, -1.0, 2.0, -2.0]], dtype=torch.float64)
+    gq = torch.tensor([[1.0, 1.0, -1.0, -1.0]], dtype=torch.float64)
+    q, st = q0.clone(), {}
+    mo.normuon_step(q, gq, st, lr=0.01, eps=0.0, weight_decay=0.5)
+    decayed = q0 * torch.tensor([[1 - 0.005, 1.0, 1.0, 1 - 0.005]], dtype=torch.float64)
+    assert torch.allclose(q, decayed - 0.01 * gq.sign(), rtol=0, atol=1e-12)
+
+
+def test_normuon_oracle_bf16_matches_fp32_reference():
+    # The bf16 path (GPU scalar semantics, per-operation rounding) stays
+    # within bf16 rounding of the reference's fp32 operations on the same
+    # bf16-valued inputs (a dropped bias correction or a wrong scalar would not).
+    g = torch.Generator().manual_seed(2)
+    p16 = (torch.randn(16, 64, generator=g) * 0.02).bfloat16()
+    g16 = (torch.randn(16, 64, generator=g) * 1e-3).bfloat16()
+    p32, s16, s32 = p16.float(), {}, {}
+    mo.normuon_step(p16, g16, s16, lr=0.02, weight_decay=0.1)
+    mo.normuon_step(p32, g16.float(), s32, lr=0.02, weight_decay=0.1)
+    assert torch.allclose(s16["exp_avg"].float(), s32["exp_avg"], rtol=2 ** -7, atol=0)
+    assert torch.allclose(s16["exp_avg_sq"].float(), s32["exp_avg_sq"], rtol=2 ** -7, atol=0)
+    assert torch.allclose(p16.float(), p32, rtol=2 ** -7, atol=0.02 * 2 ** -6)
