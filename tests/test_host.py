@@ -186,3 +186,20 @@ def test_swiglu_and_dense_ffn_interface():
             "w1.weight": (128, 64), "w2.weight": (64, 128), "w3.weight": (128, 64)}
         with pytest.raises(RuntimeError):
             e(torch.randn(5, 64))
+
+
+def test_checkpoint_round_trip_keeps_reference_layout(tmp_path):
+    # training/checkpoint.py:27-28,45-50: the model state goes to safetensors
+    # as {name: bf16 contiguous tensor}; the drop-in's keys and shapes are the
+    # reference's, so a checkpoint written from one loads into the other.
+    from safetensors.torch import load_file, save_file
+    torch.manual_seed(0)
+    a = DeepSeekMoE(configs.C2.moe_config())
+    state = {k: v.contiguous().to(torch.bfloat16) for k, v in a.state_dict().items()}
+    save_file(state, str(tmp_path / "model.safetensors"))
+    b = DeepSeekMoE(configs.C2.moe_config())
+    missing, unexpected = b.load_state_dict(load_file(str(tmp_path / "model.safetensors")), strict=True)
+    assert not missing and not unexpected
+    for k, v in b.state_dict().items():
+        assert torch.equal(v, state[k].float()), k
+    assert sorted(state) == sorted(dict(a.named_parameters()))
