@@ -30,6 +30,17 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 }
 __device__ __forceinline__ float bf_round(float f) { return bf2f(f2bf(f)); }
 
+// Round two floats to bf16 with one packed conversion (round to nearest
+// even) and return them as floats.
+__device__ __forceinline__ void bf_round2(float& x, float& y) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 r = __builtin_convertvector((f32x2){x, y}, bf16x2);
+  const uint32_t u = __builtin_bit_cast(uint32_t, r);
+  x = __uint_as_float(u << 16);
+  y = __uint_as_float(u & 0xffff0000u);
+}
+
 // Unpack 8 bf16 held in a uint4 into floats.
 __device__ __forceinline__ void unpack8(const uint4& v, float* f) {
   f[0] = __uint_as_float(v.x << 16); f[1] = __uint_as_float(v.x & 0xffff0000u);

@@ -375,17 +375,18 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
           }
         }
         // stage rows 16 i .. 16 i + 15 of the wave block, 128 accumulator columns
-        // (256 bytes per row; chunk c of row r at slot c ^ r)
+        // (256 bytes per row; chunk c of row r at slot c ^ r); GATEUP_FWD keeps
+        // the packed a | b values for h below
+        uint2 pk[FN];
         {
           const int r = el & 15;
   #pragma unroll
           for (int j = 0; j < FN; ++j) {
             const int col = j * 16 + (el >> 4) * 4;
             const uint32_t off = r * 256 + ((((col >> 3) ^ r)) << 4) + (col & 7) * 2;
-            uint2 v;
-            v.x = pack2(acc[i][j][0], acc[i][j][1]);
-            v.y = pack2(acc[i][j][2], acc[i][j][3]);
-            *reinterpret_cast<uint2*>(ep + off) = v;
+            pk[j].x = pack2(acc[i][j][0], acc[i][j][1]);
+            pk[j].y = pack2(acc[i][j][2], acc[i][j][3]);
+            *reinterpret_cast<uint2*>(ep + off) = pk[j];
           }
         }
   #pragma unroll
@@ -410,12 +411,18 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
               unpack8(pa[t], af);
               unpack8(pb[t], bfv);
   #pragma unroll
-              for (int e = 0; e < 8; ++e) {
-                const float sg = fast_sigmoid(af[e]);
-                const float sv = bf_round(af[e] * sg);
-                const float ds = bf_round(dh[e] * bfv[e]);
-                da[e] = ds * (sg * (1.0f + af[e] * (1.0f - sg)));
-                db[e] = dh[e] * sv;
+              for (int e = 0; e < 8; e += 2) {
+                // silu(a) = a * sg (sv: rounded); silu'(a) = sg * (1 + a (1 - sg))
+                // = sg + silu(a) * (1 - sg)
+                const float sg0 = fast_sigmoid(af[e]), sg1 = fast_sigmoid(af[e + 1]);
+                const float sa0 = af[e] * sg0, sa1 = af[e + 1] * sg1;
+                float sv0 = sa0, sv1 = sa1, ds0 = dh[e] * bfv[e], ds1 = dh[e + 1] * bfv[e + 1];
+                bf_round2(sv0, sv1);
+                bf_round2(ds0, ds1);
+                da[e] = ds0 * fmaf(sa0, 1.0f - sg0, sg0);
+                da[e + 1] = ds1 * fmaf(sa1, 1.0f - sg1, sg1);
+                db[e] = dh[e] * sv0;
+                db[e + 1] = dh[e + 1] * sv1;
               }
               store16(args.c0 + grow * args.ldc0 + hc, pack8(da), true);
               store16(args.c0 + grow * args.ldc0 + args.inter + hc, pack8(db), true);
@@ -432,13 +439,18 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
           const int r = el & 15;
   #pragma unroll
           for (int j = 0; j < 4; ++j) {
+            // a = bf16(acc) and b likewise, as staged above
+            const float a[4] = {__uint_as_float(pk[j].x << 16), __uint_as_float(pk[j].x & 0xffff0000u),
+                                __uint_as_float(pk[j].y << 16), __uint_as_float(pk[j].y & 0xffff0000u)};
+            const float b[4] = {__uint_as_float(pk[j + 4].x << 16), __uint_as_float(pk[j + 4].x & 0xffff0000u),
+                                __uint_as_float(pk[j + 4].y << 16), __uint_as_float(pk[j + 4].y & 0xffff0000u)};
             float hv[4];
   #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float a = bf_round(acc[i][j][e]);
-              const float b = bf_round(acc[i][j + 4][e]);
-              hv[e] = bf_round(a * fast_sigmoid(a)) * b;
-            }
+            for (int e = 0; e < 4; ++e) hv[e] = a[e] * fast_sigmoid(a[e]);
+            bf_round2(hv[0], hv[1]);
+            bf_round2(hv[2], hv[3]);
+  #pragma unroll
+            for (int e = 0; e < 4; ++e) hv[e] = hv[e] * b[e];
             const int col = j * 16 + (el >> 4) * 4;
             const uint32_t off = r * 128 + ((((col >> 3) ^ swz(r))) << 4) + (col & 7) * 2;
             uint2 v;
