@@ -49,6 +49,8 @@ def parse():
     p.add_argument("--cpu-tokens", type=int, default=2048, help="token sample for the CPU baseline")
     p.add_argument("--fwd-only", action="store_true",
                    help="time the forward pass alone (decode-shaped C3 configs); not the headline metric")
+    p.add_argument("--graph", action="store_true",
+                   help="with --fwd-only: time HIP-graph replays of the forward (DecodeGraph)")
     p.add_argument("--optimizer", action="store_true",
                    help="time the fused NorMuon step on the block's weight matrices (fp32, as the trainer "
                         "keeps them) instead of the block; its own JSON line")
@@ -352,6 +354,19 @@ def main():
     # (the roofline figures).  A forward-only (decode-sized) run is host-bound,
     # where even those events add host time: it is timed bare, and its
     # roofline comes from the table pass.
+    if args.graph:
+        # Decode as a serving loop runs it: the forward captured once into a
+        # HIP graph, each step copies the tokens in and replays it.
+        if not args.fwd_only or norms:
+            raise SystemExit("--graph times the single-block forward: use it with --fwd-only on C1..C3/C5")
+        from fusionllm_amd import DecodeGraph
+        graph = DecodeGraph(mods[0], x.detach())
+        xin = x.detach()
+
+        def step():
+            graph(xin)
+        for _ in range(args.warmup):
+            step()
     timer = {}
     K.set_timer(None if args.fwd_only else timer, only={dom})
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -406,7 +421,8 @@ def main():
         "config": {"workload": cfg.name, "tokens": T, "dim": cfg.dim, "inter": cfg.inter,
                    "experts": cfg.n_experts, "topk": cfg.topk, "shared": int(cfg.n_shared > 0),
                    "bias": cfg.bias, "layers": cfg.layers,
-                   "pass": "forward" if args.fwd_only else "forward+backward"},
+                   "pass": "forward" if args.fwd_only else "forward+backward",
+                   "launch": "hip-graph replay" if args.graph else "eager"},
         "grouped_gemm_mfma_frac": round(gemm_flops / gemm_s / PEAK_BF16_FLOPS, 4),
         "step_mfma_frac": round(gemm_flops / (elapsed / args.steps) / PEAK_BF16_FLOPS, 4),
         "roofline": roofline,

@@ -6,6 +6,7 @@ computed by hand-written gfx950 HIP kernels (libfusionmoe.so, C ABI in
 include/fusionmoe.h); ``moe_residual`` runs FusionLLMBlock's FFN half
 x + ffn(norm2(x)) with the RMSNorm and the residual fused into the kernels.
 """
+from .graph import DecodeGraph
 from .moe import DeepSeekMoE, DenseFFN, SwiGLUExpert, dense_swiglu, moe_residual
 
-__all__ = ["DeepSeekMoE", "DenseFFN", "SwiGLUExpert", "dense_swiglu", "moe_residual"]
+__all__ = ["DecodeGraph", "DeepSeekMoE", "DenseFFN", "SwiGLUExpert", "dense_swiglu", "moe_residual"]

@@ -160,6 +160,77 @@ __global__ __launch_bounds__(256) void dispatch_gather_kernel(
   x_perm[g] = x[(slot / k) * chunks + c];
 }
 
+// Decode-sized batches (n_slots <= kSmallSlots): the four stages in one
+// launch.  Every workgroup ranks all the slots (one per thread, the ballot
+// ranking of dispatch_scatter_kernel over the block's waves) and so knows the
+// whole permutation; workgroup 0 writes counts, offsets, perm and
+// pos_of_slot, and workgroup b copies rows kSmallRowsPerBlock * b .. + that
+// many of x_perm.  Same counting sort, same output.
+constexpr int kSmallSlots = kDispThreads;
+constexpr int kSmallRowsPerBlock = 16;
+
+__global__ __launch_bounds__(kDispThreads) void dispatch_small_kernel(
+    const int32_t* __restrict__ idx, int n_slots, int E, int k, const uint4* __restrict__ x, int chunks,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
+    int32_t* __restrict__ pos_of_slot, uint4* __restrict__ x_perm) {
+  __shared__ int wcount[kDispWaves][FMOE_MAX_EXPERTS];
+  __shared__ int start[FMOE_MAX_EXPERTS + 1];
+  __shared__ int perm_sh[kSmallSlots];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool first = blockIdx.x == 0;
+  for (int i = threadIdx.x; i < kDispWaves * E; i += blockDim.x) wcount[i / E][i % E] = 0;
+  __syncthreads();
+  const int s = threadIdx.x;
+  const int e_raw = s < n_slots ? idx[s] : -1;
+  const bool valid = static_cast<unsigned>(e_raw) < static_cast<unsigned>(E);
+  const int e = valid ? e_raw : -1;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  uint64_t pending = __ballot(valid);
+  int rank = 0;
+  while (pending) {
+    const int leader = __ffsll(static_cast<unsigned long long>(pending)) - 1;
+    const int le = __shfl(e, leader);
+    const uint64_t m = __ballot(e == le);
+    if (e == le) rank = __popcll(m & lt_mask);
+    if (lane == leader) wcount[wave][le] = __popcll(m);
+    pending &= ~m;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int q = 0; q < E; ++q) {
+      start[q] = run;
+      for (int w = 0; w < kDispWaves; ++w) run += wcount[w][q];
+    }
+    start[E] = run;
+  }
+  __syncthreads();
+  if (valid) {
+    int pos = start[e] + rank;
+    for (int w = 0; w < wave; ++w) pos += wcount[w][e];
+    perm_sh[pos] = s;
+    if (first) {
+      perm[pos] = s;
+      pos_of_slot[s] = pos;
+    }
+  }
+  if (first) {
+    for (int q = threadIdx.x; q < E; q += blockDim.x) {
+      counts[q] = start[q + 1] - start[q];
+      offsets[q] = start[q];
+    }
+    if (threadIdx.x == 0) offsets[E] = start[E];
+  }
+  if (x_perm == nullptr) return;
+  __syncthreads();
+  const int r0 = blockIdx.x * kSmallRowsPerBlock;
+  const int r1 = min(r0 + kSmallRowsPerBlock, start[E]);  // rows that hold a slot
+  for (int g = r0 * chunks + threadIdx.x; g < r1 * chunks; g += blockDim.x) {
+    const int r = g / chunks, c = g - r * chunks;
+    x_perm[static_cast<int64_t>(r) * chunks + c] = x[static_cast<int64_t>(perm_sh[r] / k) * chunks + c];
+  }
+}
+
 }  // namespace fmoe
 
 using namespace fmoe;
@@ -190,6 +261,14 @@ extern "C" int fmoe_dispatch(const int32_t* idx, const void* x, int64_t T, int64
   if (!idx || !x || !perm || !pos_of_slot || !workspace) return FMOE_ERR_INVALID_ARG;
   if (workspace_bytes < fmoe_dispatch_workspace_bytes(T, n_experts, k)) return FMOE_ERR_WORKSPACE;
   if (!aligned16(x) || (x_perm && !aligned16(x_perm))) return FMOE_ERR_ALIGN;
+  if (n_slots <= kSmallSlots) {
+    const int chunks = static_cast<int>(dim / 8);
+    const int64_t blocks = x_perm ? ceil_div(n_slots, kSmallRowsPerBlock) : 1;
+    dispatch_small_kernel<<<dim3(blocks), dim3(kDispThreads), 0, s>>>(
+        idx, (int)n_slots, n_experts, k, static_cast<const uint4*>(x), chunks, counts, offsets, perm,
+        pos_of_slot, static_cast<uint4*>(x_perm));
+    return launch_status();
+  }
   int32_t* block_hist = static_cast<int32_t*>(workspace);
   int32_t* block_base = block_hist + nblocks * n_experts;
   dispatch_hist_kernel<<<dim3(nblocks), dim3(kDispThreads), 0, s>>>(idx, (int)n_slots, n_experts,

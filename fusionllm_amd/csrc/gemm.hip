@@ -516,21 +516,35 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 
 // ---- small groups (decode-sized batches) -------------------------------------
 // A group of at most kSmallM rows would leave a 256 x 256 tile nearly empty
-// and run its whole K loop in one workgroup.  Here one workgroup owns a block
-// of 32 output columns of one group (GATEUP_FWD: 16 h columns, i.e. 16 rows
-// of w1 and the same 16 rows of w3), its 4 waves split K in four, stream
-// their MFMA fragments straight from memory (the weights are read once), and
-// the four partial tiles are added in wave order through LDS.
+// and run its whole K loop in one workgroup; such a product is bound by
+// streaming the weights, so the aim is to have all of them in flight at once.
+// One workgroup owns 16 output columns of one group (GATEUP_FWD: 16 h
+// columns, i.e. the same 16 rows of w1 and of w3, two accumulators); its
+// waves (4 for the gate/up product, 8 for the down product, whose K is the
+// longer one in the reference's shapes: the faster counts measured) split the K steps of 32 evenly, and
+// each wave issues the loads of up to CH steps before their MFMAs
+// (v_mfma_f32_16x16x32_bf16, operands read straight from memory: the weights
+// once, the few activation rows from L2).  The partial tiles are added in
+// wave order through LDS.  MB = 16-row blocks the kernel is built for (the
+// host picks it from a bound on the group sizes; with MB > 2 fewer K steps
+// are in flight, the activation fragments take the registers).  Rows past a
+// group's end repeat its last row and are not stored.
 constexpr int kSmallM = 128;
-constexpr int kSmallMB = kSmallM / 32;
-constexpr int kSmallUnroll = 4;
 
 template <int MODE>
-__global__ __launch_bounds__(256) void small_gemm_kernel(const GemmArgs args) {
+constexpr int small_waves() { return MODE == GATEUP_FWD ? 4 : 8; }
+
+template <int MODE, int MB>
+__global__ __launch_bounds__(small_waves<MODE>() * 64) void small_gemm_kernel(const GemmArgs args) {
   static_assert(MODE == GATEUP_FWD || MODE == DOWN_FWD, "forward products only");
-  __shared__ float red[4][kSmallMB][16][64];  // [wave][m block][register][lane]
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int ncb = (MODE == GATEUP_FWD) ? args.N / 16 : args.N / 32;
+  constexpr int kSmallWaves = small_waves<MODE>();
+  constexpr int NB = (MODE == GATEUP_FWD) ? 2 : 1;  // weight matrices (accumulators per m block)
+  constexpr int CH = MB <= 2 ? 8 : (MB == 4 ? 4 : 2);
+  constexpr int PASS = 2;  // m blocks reduced per LDS pass
+  __shared__ float red[kSmallWaves][PASS][NB][4][64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ncb = args.N / 16;
   const int g = blockIdx.x / ncb, cb = blockIdx.x % ncb;
   int row_base, M;
   if (g < args.E) {
@@ -544,81 +558,100 @@ __global__ __launch_bounds__(256) void small_gemm_kernel(const GemmArgs args) {
   const uint16_t* A = (g < args.E || args.a_shared == nullptr)
                           ? args.a_routed + static_cast<int64_t>(row_base) * args.lda
                           : args.a_shared;
-  // B fragment column j = lane % 32: the weight row this lane streams
-  const int j = lane & 31, kh = (lane >> 5) * 8;
-  const uint16_t* wrow;
-  if constexpr (MODE == GATEUP_FWD)
-    wrow = (j < 16 ? args.b0[g] : args.b1[g]) + static_cast<int64_t>(cb * 16 + (j & 15)) * args.ldb;
-  else
-    wrow = args.b0[g] + static_cast<int64_t>(cb * 32 + j) * args.ldb;
-  const int mb_n = (M + 31) / 32;  // 1 .. kSmallMB
-  const uint16_t* ap[kSmallMB];
+  // Fragments (operands swapped: srcA = weight rows, srcB = activation rows):
+  // lane l supplies row l % 16 of each, K elements 8 (l / 16) .. +7 of a step,
+  // and gets C[m = l % 16][n = 4 (l / 16) + 0..3].
+  const int r16 = lane & 15, kq = (lane >> 4) * 8;
+  const uint16_t* w0 = args.b0[g] + static_cast<int64_t>(cb * 16 + r16) * args.ldb + kq;
+  const uint16_t* w1 = (MODE == GATEUP_FWD) ? args.b1[g] + static_cast<int64_t>(cb * 16 + r16) * args.ldb + kq
+                                            : nullptr;
+  const int mb_n = (M + 15) / 16;  // 1 .. MB
+  const uint16_t* ap[MB];
 #pragma unroll
-  for (int mb = 0; mb < kSmallMB; ++mb) {
-    const int r = min(32 * mb + j, M - 1);  // rows past M repeat the last row
-    ap[mb] = A + static_cast<int64_t>(r) * args.lda + kh;
-  }
-  const int kq = args.K / 4;  // a multiple of 16
-  const int k_begin = wave * kq, k_end = k_begin + kq;
+  for (int mb = 0; mb < MB; ++mb)
+    ap[mb] = A + static_cast<int64_t>(min(16 * mb + r16, M - 1)) * args.lda + kq;
+  const int nsteps = args.K / 32;
+  const int s_begin = wave * nsteps / kSmallWaves, s_end = (wave + 1) * nsteps / kSmallWaves;
 
-  f32x16 acc[kSmallMB];
+  f32x4 acc[MB][NB];
 #pragma unroll
-  for (int mb = 0; mb < kSmallMB; ++mb)
+  for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[mb][r] = 0.0f;
-  for (int k0 = k_begin; k0 < k_end; k0 += 16 * kSmallUnroll) {
-    bf16x8 bf[kSmallUnroll], af[kSmallUnroll][kSmallMB];
+    for (int b = 0; b < NB; ++b) acc[mb][b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = s_begin; s0 < s_end; s0 += CH) {
+    bf16x8 bw[CH][NB], af[CH][MB];
 #pragma unroll
-    for (int u = 0; u < kSmallUnroll; ++u) {
-      const int kk = k0 + 16 * u;
-      if (kk < k_end) {
-        bf[u] = *reinterpret_cast<const bf16x8*>(wrow + kk + kh);
+    for (int u = 0; u < CH; ++u) {
+      if (s0 + u < s_end) {
+        const int k = 32 * (s0 + u);
+        bw[u][0] = *reinterpret_cast<const bf16x8*>(w0 + k);
+        if constexpr (NB == 2) bw[u][1] = *reinterpret_cast<const bf16x8*>(w1 + k);
 #pragma unroll
-        for (int mb = 0; mb < kSmallMB; ++mb)
-          if (mb < mb_n) af[u][mb] = *reinterpret_cast<const bf16x8*>(ap[mb] + kk);
+        for (int mb = 0; mb < MB; ++mb)
+          if (mb < mb_n) af[u][mb] = *reinterpret_cast<const bf16x8*>(ap[mb] + k);
       }
     }
 #pragma unroll
-    for (int u = 0; u < kSmallUnroll; ++u) {
-      if (k0 + 16 * u < k_end) {
+    for (int u = 0; u < CH; ++u) {
+      if (s0 + u < s_end) {
 #pragma unroll
-        for (int mb = 0; mb < kSmallMB; ++mb)
-          if (mb < mb_n) acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[u][mb], bf[u], acc[mb], 0, 0, 0);
+        for (int mb = 0; mb < MB; ++mb)
+          if (mb < mb_n)
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+              acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw[u][b], af[u][mb], acc[mb][b], 0, 0, 0);
       }
     }
   }
+  // Passes of PASS m blocks: every wave parks its partials, wave p of the pass
+  // adds the eight partials of m block (pass base + p) in wave order and stores.
+  const int m = lane & 15, n0 = cb * 16 + (lane >> 4) * 4;
+  for (int base = 0; base < mb_n; base += PASS) {
 #pragma unroll
-  for (int mb = 0; mb < kSmallMB; ++mb)
-    if (mb < mb_n)
+    for (int p = 0; p < PASS; ++p) {
+      const int mb = base + p;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) red[wave][mb][r][lane] = acc[mb][r];
-  __syncthreads();
-  // wave w finishes m blocks w, w + 4, ...: the four partials in wave order
-  for (int mb = wave; mb < mb_n; mb += 4) {
+      for (int q = 0; q < MB; ++q)  // static register index
+        if (q == mb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float v = red[0][mb][r][lane];
-      v = v + red[1][mb][r][lane];
-      v = v + red[2][mb][r][lane];
-      v = v + red[3][mb][r][lane];
-      // lane holds C[m = 32 mb + 8 (r / 4) + 4 (lane / 32) + r % 4][n = lane % 32]
-      const int m = 32 * mb + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-      const int64_t row = row_base + m;
-      if constexpr (MODE == GATEUP_FWD) {
-        // lanes j < 16 hold a, lanes j + 16 hold b for the same h column
-        const float a = bf_round(v);
-        const float b = __shfl(a, (lane & 32) + (j & 15) + 16, 64);
-        if (m < M && j < 16) {
-          const int col = cb * 16 + j;
-          const float sv = bf_round(a * fast_sigmoid(a));
-          args.c0[row * args.ldc0 + col] = f2bf(a);
-          args.c0[row * args.ldc0 + args.inter + col] = f2bf(b);
-          args.c1[row * args.ldc1 + col] = f2bf(sv * b);
+          for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wave][p][b][r][lane] = acc[q][b][r];
+    }
+    __syncthreads();
+    const int mb = base + wave;
+    if (wave < PASS && mb < mb_n && 16 * mb + m < M) {
+      float v[NB][4];
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float t = red[0][wave][b][r][lane];
+#pragma unroll
+          for (int w = 1; w < kSmallWaves; ++w) t = t + red[w][wave][b][r][lane];
+          v[b][r] = t;
         }
+      const int64_t row = row_base + 16 * mb + m;
+      if constexpr (MODE == GATEUP_FWD) {
+        float hv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          v[0][r] = bf_round(v[0][r]);
+          v[1][r] = bf_round(v[1][r]);
+          hv[r] = bf_round(v[0][r] * fast_sigmoid(v[0][r])) * v[1][r];
+        }
+        uint16_t* ab = args.c0 + row * args.ldc0;
+        *reinterpret_cast<uint2*>(ab + n0) = make_uint2(pack2(v[0][0], v[0][1]), pack2(v[0][2], v[0][3]));
+        *reinterpret_cast<uint2*>(ab + args.inter + n0) =
+            make_uint2(pack2(v[1][0], v[1][1]), pack2(v[1][2], v[1][3]));
+        *reinterpret_cast<uint2*>(args.c1 + row * args.ldc1 + n0) =
+            make_uint2(pack2(hv[0], hv[1]), pack2(hv[2], hv[3]));
       } else {
-        if (m < M) args.c0[row * args.ldc0 + cb * 32 + j] = f2bf(v);
+        *reinterpret_cast<uint2*>(args.c0 + row * args.ldc0 + n0) =
+            make_uint2(pack2(v[0][0], v[0][1]), pack2(v[0][2], v[0][3]));
       }
     }
+    __syncthreads();
   }
 }
 
@@ -927,27 +960,45 @@ int device_cus() {
   return v;
 }
 
+// 16-row blocks of the small-group kernel for a launch whose groups have at
+// most max_rows rows (a power of two, 1 .. kSmallM / 16).
+inline int small_blocks(int64_t max_rows) {
+  const int64_t mb = ceil_div(max_rows < kSmallM ? max_rows : kSmallM, 16);
+  return mb <= 1 ? 1 : mb <= 2 ? 2 : mb <= 4 ? 4 : 8;
+}
+
 template <int MODE>
 int launch_rows(GemmArgs& a, int64_t rows_routed, int64_t rows_shared, int E, void* stream) {
   constexpr int TN_COLS = (MODE == GATEUP_FWD) ? core::BN / 2 : core::BN;
   const int64_t tiles_n = ceil_div(a.N, TN_COLS);
   constexpr bool kHasSmall = (MODE == GATEUP_FWD || MODE == DOWN_FWD);
   a.small_max = (kHasSmall && rows_routed + rows_shared <= kSmallLaunchRows) ? kSmallM : 0;
+  // A routed group has at most rows_routed rows: when no group can exceed
+  // small_max, the tiled kernel (and its split reduction) has nothing to do.
+  const bool all_small = a.small_max > 0 && rows_routed <= a.small_max && rows_shared <= a.small_max;
   // Upper bound of sum over groups of ceil(M_g / BM): floor(rows/BM) + groups.
   const int64_t tiles = (rows_routed / core::BM + E + ceil_div(rows_shared, core::BM)) * tiles_n;
   if (tiles <= 0) return FMOE_OK;
-  const int64_t grid = tiles < device_cus() ? tiles : device_cus();
-  rows_gemm_kernel<MODE><<<dim3(grid), dim3(core::NT), 0, as_stream(stream)>>>(a, a.offsets);
-  if constexpr (MODE == DOWN_FWD || MODE == GATEUP_BWD) {
-    if (a.split_ws != nullptr)
-      split_reduce_kernel<<<dim3(grid * 8), dim3(256), 0, as_stream(stream)>>>(a.split_ws, static_cast<int>(grid),
-                                                                               a.c0, a.ldc0);
+  if (!all_small) {
+    const int64_t grid = tiles < device_cus() ? tiles : device_cus();
+    rows_gemm_kernel<MODE><<<dim3(grid), dim3(core::NT), 0, as_stream(stream)>>>(a, a.offsets);
+    if constexpr (MODE == DOWN_FWD || MODE == GATEUP_BWD) {
+      if (a.split_ws != nullptr)
+        split_reduce_kernel<<<dim3(grid * 8), dim3(256), 0, as_stream(stream)>>>(a.split_ws, static_cast<int>(grid),
+                                                                                 a.c0, a.ldc0);
+    }
   }
   if constexpr (kHasSmall) {
     if (a.small_max > 0) {
       const int G = E + (rows_shared > 0 ? 1 : 0);
-      const int64_t ncb = (MODE == GATEUP_FWD) ? a.N / 16 : a.N / 32;
-      small_gemm_kernel<MODE><<<dim3(G * ncb), dim3(256), 0, as_stream(stream)>>>(a);
+      const dim3 grid(G * (a.N / 16)), block(small_waves<MODE>() * 64);
+      hipStream_t s = as_stream(stream);
+      switch (small_blocks(rows_routed > rows_shared ? rows_routed : rows_shared)) {
+        case 1: small_gemm_kernel<MODE, 1><<<grid, block, 0, s>>>(a); break;
+        case 2: small_gemm_kernel<MODE, 2><<<grid, block, 0, s>>>(a); break;
+        case 4: small_gemm_kernel<MODE, 4><<<grid, block, 0, s>>>(a); break;
+        default: small_gemm_kernel<MODE, 8><<<grid, block, 0, s>>>(a); break;
+      }
     }
   }
   return launch_status();

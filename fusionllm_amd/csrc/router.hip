@@ -39,6 +39,46 @@ __device__ __forceinline__ float xor_lane(float v, int off) {
   return __int_as_float(r);
 }
 
+// Scores and top-k of one token from its logits lg[0 .. E) (bias not yet
+// added), computed redundantly by the 16 lanes of the token's group; lane
+// j < k writes the j-th choice.
+template <int EB>
+__device__ __forceinline__ void route_token(const float* lg, const uint16_t* __restrict__ bg, int E, int k,
+                                            float route_scale, int lane16, bool active, int t,
+                                            int32_t* __restrict__ idx, int64_t* __restrict__ idx64,
+                                            float* __restrict__ wout, float* __restrict__ vout) {
+  float s[EB];
+#pragma unroll
+  for (int e = 0; e < EB; ++e) s[e] = (e < E) ? fm_sigmoid(lg[e] + bf2f(bg[e])) : 0.0f;
+
+  // k selection rounds (a runtime loop over the token's k); lane j keeps the
+  // j-th choice, and the chosen scores are summed in choice order.
+  uint64_t taken = 0;
+  int e_sel = 0;
+  float v_sel = 0.0f, sum = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    int best = -1;
+    float bv = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EB; ++e) {
+      if (e < E && !((taken >> e) & 1ull)) {
+        if (best < 0 || score_beats(s[e], bv)) { best = e; bv = s[e]; }
+      }
+    }
+    taken |= 1ull << best;
+    sum = (j == 0) ? bv : sum + bv;
+    if (j == lane16) { e_sel = best; v_sel = bv; }
+  }
+  const float denom = sum + 1e-10f;
+  if (active && lane16 < k) {
+    const int64_t o = static_cast<int64_t>(t) * k + lane16;
+    idx[o] = e_sel;
+    if (idx64) idx64[o] = e_sel;
+    wout[o] = (v_sel / denom) * route_scale;
+    vout[o] = v_sel;
+  }
+}
+
 template <int EB, int NQ>  // NQ: x chunks per lane, NQ * 16 * 8 >= dim
 __global__ __launch_bounds__(512) void router_fwd_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg,
@@ -101,38 +141,60 @@ __global__ __launch_bounds__(512) void router_fwd_kernel(
   }
   __syncthreads();
 
-  // Scores and top-k, computed redundantly by the 16 lanes of a token;
-  // lane j < k writes the j-th choice.
-  float s[EB];
-#pragma unroll
-  for (int e = 0; e < EB; ++e) s[e] = (e < E) ? fm_sigmoid(lsh[tl * EB + e] + bf2f(bg[e])) : 0.0f;
+  route_token<EB>(lsh + tl * EB, bg, E, k, route_scale, lane16, active, t, idx, idx64, wout, vout);
+}
 
-  // k selection rounds (a runtime loop over the token's k); lane j keeps the
-  // j-th choice, and the chosen scores are summed in choice order.
-  uint64_t taken = 0;
-  int e_sel = 0;
-  float v_sel = 0.0f, sum = 0.0f;
-  for (int j = 0; j < k; ++j) {
-    int best = -1;
-    float bv = 0.0f;
+// Decode-sized batches (T <= kRouterSmallT): one workgroup per token and one
+// 16-lane group per expert (group g takes experts g, g + G, ...), so that the
+// logits of a token are formed side by side instead of one expert after
+// another.  Each logit is summed in exactly the order described at the top
+// (the lanes of a group own the same chunks), so both kernels give the same
+// bits.  The gate rows are read from memory (L2) by every token's workgroup.
+constexpr int kRouterSmallT = 128;
+
+template <int EB, int NQ>
+__global__ __launch_bounds__(512) void router_small_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg,
+    const uint16_t* __restrict__ bg, int dim, int E, int k, float route_scale,
+    int32_t* __restrict__ idx, int64_t* __restrict__ idx64, float* __restrict__ wout,
+    float* __restrict__ vout) {
+  __shared__ float lsh[EB];
+  const int lane16 = threadIdx.x % kRouterLanes;
+  const int grp = threadIdx.x / kRouterLanes, ngrp = blockDim.x / kRouterLanes;
+  const int t = blockIdx.x;
+  const int nchunk = dim / 8;
+  const uint4* xrow = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t) * dim);
+  uint4 xr[NQ];
 #pragma unroll
-    for (int e = 0; e < EB; ++e) {
-      if (e < E && !((taken >> e) & 1ull)) {
-        if (best < 0 || score_beats(s[e], bv)) { best = e; bv = s[e]; }
+  for (int q = 0; q < NQ; ++q) {
+    const int c = lane16 + kRouterLanes * q;
+    xr[q] = c < nchunk ? xrow[c] : make_uint4(0, 0, 0, 0);
+  }
+  for (int e = grp; e < E; e += ngrp) {
+    const uint4* wrow = reinterpret_cast<const uint4*>(wg + static_cast<int64_t>(e) * dim);
+    uint4 wr[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int c = lane16 + kRouterLanes * q;
+      wr[q] = c < nchunk ? wrow[c] : make_uint4(0, 0, 0, 0);
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      if (lane16 + kRouterLanes * q < nchunk) {
+        float xf[8], wf[8];
+        unpack8(xr[q], xf);
+        unpack8(wr[q], wf);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc = fmaf(xf[i], wf[i], acc);
       }
     }
-    taken |= 1ull << best;
-    sum = (j == 0) ? bv : sum + bv;
-    if (j == lane16) { e_sel = best; v_sel = bv; }
+#pragma unroll
+    for (int off = kRouterLanes / 2; off >= 1; off >>= 1) acc = acc + xor_lane(acc, off);
+    if (lane16 == 0) lsh[e] = acc;
   }
-  const float denom = sum + 1e-10f;
-  if (active && lane16 < k) {
-    const int64_t o = static_cast<int64_t>(t) * k + lane16;
-    idx[o] = e_sel;
-    if (idx64) idx64[o] = e_sel;
-    wout[o] = (v_sel / denom) * route_scale;
-    vout[o] = v_sel;
-  }
+  __syncthreads();
+  if (grp == 0) route_token<EB>(lsh, bg, E, k, route_scale, lane16, true, t, idx, idx64, wout, vout);
 }
 
 // ---- backward ----------------------------------------------------------------
@@ -282,16 +344,24 @@ extern "C" int fmoe_router_fwd(const void* x, const void* gate_w, const void* ga
   if (T == 0) return FMOE_OK;
   if (!x || !gate_w || !gate_b || !idx || !weights || !topv) return FMOE_ERR_INVALID_ARG;
   if (!aligned16(x) || !aligned16(gate_w)) return FMOE_ERR_ALIGN;
-  const int threads = kRouterTok * kRouterLanes;
-  const int64_t blocks = ceil_div(T, kRouterTok);
+  const bool small = T <= kRouterSmallT;
+  const int threads = small ? kRouterLanes * (n_experts < 32 ? n_experts : 32) : kRouterTok * kRouterLanes;
+  const int64_t blocks = small ? T : ceil_div(T, kRouterTok);
   hipStream_t s = as_stream(stream);
   auto xs = static_cast<const uint16_t*>(x);
   auto ws = static_cast<const uint16_t*>(gate_w);
   auto bs = static_cast<const uint16_t*>(gate_b);
-#define FMOE_ROUTER_LAUNCH(EB, NQ)                                                               \
-  router_fwd_kernel<EB, NQ><<<dim3(blocks), dim3(threads), 0, s>>>(xs, ws, bs, (int)T, (int)dim, \
-                                                                   n_experts, k, route_scale,   \
-                                                                   idx, idx64, weights, topv)
+#define FMOE_ROUTER_LAUNCH(EB, NQ)                                                                    \
+  do {                                                                                                \
+    if (small)                                                                                        \
+      router_small_kernel<EB, NQ><<<dim3(blocks), dim3(threads), 0, s>>>(xs, ws, bs, (int)dim,         \
+                                                                         n_experts, k, route_scale,  \
+                                                                         idx, idx64, weights, topv); \
+    else                                                                                              \
+      router_fwd_kernel<EB, NQ><<<dim3(blocks), dim3(threads), 0, s>>>(xs, ws, bs, (int)T, (int)dim,  \
+                                                                       n_experts, k, route_scale,    \
+                                                                       idx, idx64, weights, topv);   \
+  } while (0)
 #define FMOE_ROUTER_LAUNCH_E(NQ)                 \
   do {                                           \
     if (n_experts <= 8) FMOE_ROUTER_LAUNCH(8, NQ);       \

@@ -37,7 +37,10 @@ def _check_router(x, gw, gb, k, rs, dev):
 
 
 @pytest.mark.parametrize("T,d,E,k,rs", [(2048, 768, 8, 2, 1.0), (1, 768, 8, 2, 1.0), (333, 768, 8, 2, 2.5),
-                                        (512, 2048, 64, 6, 1.0), (200, 256, 16, 4, 1.0), (64, 64, 3, 3, 1.0)])
+                                        (512, 2048, 64, 6, 1.0), (200, 256, 16, 4, 1.0), (64, 64, 3, 3, 1.0),
+                                        # decode-sized batches (one workgroup per token) and the boundary
+                                        (128, 2048, 64, 6, 1.0), (129, 768, 8, 2, 1.0), (5, 768, 8, 2, 2.5),
+                                        (17, 256, 33, 8, 1.0)])
 def test_router_bit_exact(gpu_device, T, d, E, k, rs):
     x, gw, gb = _routing_inputs(T, d, E, seed=T + E)
     _check_router(x, gw, gb, k, rs, gpu_device)
@@ -56,7 +59,9 @@ def test_router_ties_and_nan(gpu_device):
     _check_router(x, gw, gb, k, 1.0, gpu_device)
 
 
-@pytest.mark.parametrize("T,d,E,k", [(16384, 768, 8, 2), (1, 768, 8, 2), (129, 768, 8, 2), (3000, 2048, 64, 6)])
+@pytest.mark.parametrize("T,d,E,k", [(16384, 768, 8, 2), (1, 768, 8, 2), (129, 768, 8, 2), (3000, 2048, 64, 6),
+                                     # single-launch path for <= 256 slots, and its boundary
+                                     (128, 768, 8, 2), (3, 2048, 64, 6), (40, 256, 64, 6), (37, 64, 3, 3)])
 def test_dispatch_bit_exact(gpu_device, T, d, E, k):
     x, gw, gb = _routing_inputs(T, d, E, seed=7)
     xd = x.to(gpu_device)
@@ -71,13 +76,16 @@ def test_dispatch_bit_exact(gpu_device, T, d, E, k):
     assert torch.equal(x_perm.cpu().view(torch.int16), x[rp.long() // k].view(torch.int16))
 
 
-def test_dispatch_all_on_one_expert(gpu_device):
-    T, d, E, k = 5000, 64, 8, 1
+@pytest.mark.parametrize("T", [5000, 200])
+def test_dispatch_all_on_one_expert(gpu_device, T):
+    d, E, k = 64, 8, 1
     idx = torch.full((T, k), 5, dtype=torch.int32)
     x = torch.randn(T, d).bfloat16()
     counts, offsets, perm, pos, x_perm = K.dispatch(idx.to(gpu_device), x.to(gpu_device), E)
     assert counts.cpu().tolist() == [0, 0, 0, 0, 0, T, 0, 0]
     assert torch.equal(perm.cpu(), torch.arange(T, dtype=torch.int32))
+    assert torch.equal(pos.cpu(), torch.arange(T, dtype=torch.int32))
+    assert torch.equal(x_perm.cpu().view(torch.int16), x.view(torch.int16))
 
 
 # ---- grouped GEMMs -----------------------------------------------------------------
@@ -91,8 +99,12 @@ def _bf(*shape, scale=1.0, g=None):
     return (torch.randn(*shape, generator=g) * scale).bfloat16()
 
 
-@pytest.mark.parametrize("counts,shared,d,I", [([0, 300, 517], 400, 192, 320), ([1, 2, 700], 0, 768, 2048),
-                                               ([256, 256], 256, 256, 128)])
+@pytest.mark.parametrize("counts,shared,d,I", [
+    ([0, 300, 517], 400, 192, 320), ([1, 2, 700], 0, 768, 2048), ([256, 256], 256, 256, 128),
+    # decode-sized launches (groups of <= 128 rows go to the small-group kernel,
+    # built for 1, 2, 4 or 8 blocks of 16 rows from a bound on the group sizes)
+    ([0, 1], 1, 256, 128), ([1, 0, 0, 1, 0, 0, 0, 0], 1, 768, 2048), ([1, 5, 16, 17], 32, 768, 2048),
+    ([33, 64, 100, 128, 7], 128, 192, 320), ([129, 3, 0], 2, 256, 512), ([2], 0, 2048, 1408)])
 def test_gateup_and_down_fwd(gpu_device, counts, shared, d, I):
     g = torch.Generator().manual_seed(1)
     E = len(counts)
