@@ -74,11 +74,23 @@ def copy_calibration():
     print(json.dumps({"copy_bytes": COPY_BYTES, "copies": 3}), flush=True)
 
 
-def kernel_model(cfg, T):
+def kernel_model(cfg, T, active_groups=None):
     """Algorithmic work per launch of each entry point (FLOPs for the GEMMs,
-    bytes for the memory-bound kernels) at T tokens."""
+    bytes for the memory-bound kernels) at T tokens.  Decode-sized batches
+    (T <= 128, every group <= 128 rows: the weight-streaming kernel) price the
+    forward products by HBM bytes: the weights of the active_groups groups
+    that received rows (shared expert included), read once, plus the
+    activation rows in and out."""
     d, I, E, k = cfg.dim, cfg.inter, cfg.n_experts, cfg.topk
     rows = T * k + (T if cfg.n_shared else 0)
+    if T <= 128 and active_groups is not None:
+        return {
+            "gateup_fwd": ("hbm", active_groups * 2 * I * d * 2 + rows * (d + 3 * I) * 2),
+            "down_fwd": ("hbm", active_groups * d * I * 2 + rows * (I + d) * 2),
+            "router_fwd": ("hbm", T * (2 * d + 4 * k + 8 * k + 4 * k + 4 * k) + E * (d + 1) * 2),
+            "dispatch": ("hbm", T * (4 * k + 2 * d + k * 2 * d + 8 * k + 4 * k)),
+            "combine_fwd": ("hbm", T * (k * 2 * d + 2 * d + 8 * k + 4 * k + 2 * d)),
+        }
     return {
         # MFMA-bound products (FLOPs)
         "gateup_fwd": ("mfma", 2.0 * rows * d * 2 * I),
@@ -100,6 +112,59 @@ def kernel_model(cfg, T):
         "dx_reduce_norm": ("hbm", T * (k * 2 * d + 2 * d + 2 * d + 2 * d + 2 * d + 12 * k + 4)),
         "transpose_weights": ("hbm", (E + (1 if cfg.n_shared else 0)) * 3 * d * I * 2 * 2),
     }
+
+
+def graph_entry_times(m, x, reps=20, replays=20):
+    """Per-launch time (us) of each forward entry point of the DeepSeekMoE
+    block on input x, measured the way a HIP-graph replay runs it: a graph of
+    `reps` back-to-back launches of one entry point (same inputs), replayed
+    `replays` times between two HIP events on the replaying stream.  Events
+    cannot be recorded inside a captured graph, so the per-entry-point figures
+    of a graph-replayed forward come from these graphs."""
+    from fusionllm_amd import _kernels as K
+    from fusionllm_amd.moe import _forward_pass
+    E, k = m.n_routed_experts, m.n_activated_experts
+    has_shared = m.shared_expert is not None
+    meta = (E, k, m.moe_inter_dim, float(m.route_scale), has_shared, x.dtype)
+    with torch.no_grad():
+        fw = _forward_pass(meta, x, m.gate.weight, m.gate.bias, m._flat_weights())
+    xb, gwb, wb, idx, idx64, w, v, counts, offsets, perm, pos, x_perm, ab, h, o, y = fw
+    T, d = xb.shape
+    G = E + (1 if has_shared else 0)
+    w1s, w3s, w2s = wb[0::3][:G], wb[1::3][:G], wb[2::3][:G]
+    gbb = m.gate.bias.to(torch.bfloat16).contiguous()
+    rows_r, rows_s = T * k, (T if has_shared else 0)
+    calls = {
+        "router_fwd": lambda: K.router_fwd(xb, gwb, gbb, k, float(m.route_scale)),
+        "dispatch": lambda: K.dispatch(idx, xb, E),
+        "gateup_fwd": lambda: K.gateup_fwd(x_perm, xb if has_shared else None, offsets, E, w1s, w3s,
+                                           m.moe_inter_dim),
+        "down_fwd": lambda: K.down_fwd(h, offsets, E, rows_r, rows_s, w2s, d),
+        "combine_fwd": lambda: K.combine_fwd(o, idx, w, pos, rows_r, has_shared, x.dtype, None),
+    }
+    out = {}
+    for name, fn in calls.items():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(replays):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        out[name] = a.elapsed_time(b) * 1e3 / (reps * replays)
+        del g
+    return out
 
 
 def hbm_traffic(cfg_name, entry):
@@ -312,7 +377,11 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    model = kernel_model(cfg, T)
+    # groups that received rows in this workload's routing (decode pricing)
+    active = None
+    if not norms and mods[0]._last_counts is not None:
+        active = int((mods[0]._last_counts > 0).sum()) + (1 if cfg.n_shared else 0)
+    model = kernel_model(cfg, T, active)
 
     def table_of(timer, n_steps, span_s):
         """Per-entry-point figures from HIP-event pairs."""
@@ -382,6 +451,24 @@ def main():
     gpu_s = start.elapsed_time(end) / 1e3
     elapsed = max(gpu_s, wall)
     tok_s = T * args.steps / elapsed
+    if args.graph:
+        # Per-entry-point figures of the replayed forward: graphs of
+        # back-to-back launches of each entry point (the eager table pass
+        # above measures host-bound launches).
+        step_us = elapsed / args.steps * 1e6
+        kernels = {}
+        for name, us in graph_entry_times(mods[0], x.detach()).items():
+            bound, work = model.get(name, (None, None))
+            e = {"avg_us": round(us, 2), "calls": "graph", "share": round(us / step_us, 4)}
+            if bound == "hbm":
+                e.update(bound="hbm", achieved_gbs=round(work / (us / 1e6) / 1e9, 1),
+                         frac=round(work / (us / 1e6) / PEAK_HBM_BYTES, 4))
+            elif bound == "mfma":
+                e.update(bound="mfma", achieved_tflops=round(work / (us / 1e6) / 1e12, 1),
+                         frac=round(work / (us / 1e6) / PEAK_BF16_FLOPS, 4))
+            kernels[name] = e
+        dom = max(kernels, key=lambda n: kernels[n]["share"])
+        timer = {}
     dk = (table_of(timer, args.steps, elapsed) if timer else kernels)[dom]
 
     bound, work = model[dom]
@@ -395,8 +482,9 @@ def main():
         roofline = {"kernel": dom, "bound": "hbm", "achieved": round(work / avg_s / 1e9, 1),
                     "peak": PEAK_HBM_BYTES / 1e9, "unit": "GB/s", "frac": round(work / avg_s / PEAK_HBM_BYTES, 4),
                     "traffic": traffic, "work_per_launch": work, "launches_timed": dk["calls"]}
-    gemm_s = sum(kernels[n]["avg_us"] * kernels[n]["calls"] for n in kernels if model.get(n, ("",))[0] == "mfma")
-    gemm_s = gemm_s / 1e6 / table_steps
+    gemm_names = ("gateup_fwd", "down_fwd", "down_bwd_dx", "gateup_bwd_dx", "weight_grad:w2", "weight_grad:w13")
+    gemm_s = sum(kernels[n]["avg_us"] * (1 if args.graph else kernels[n]["calls"] / table_steps)
+                 for n in kernels if n in gemm_names) / 1e6
     gemm_flops = cfg.flops_fwd_bwd() / (3.0 if args.fwd_only else 1.0)
 
     cpu = None
