@@ -521,11 +521,11 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 // One workgroup owns 16 output columns of one group (GATEUP_FWD: 16 h
 // columns, i.e. the same 16 rows of w1 and of w3, two accumulators); its
 // waves (4 for the gate/up product, 8 for the down product, whose K is the
-// longer one in the reference's shapes: the faster counts measured) split the K steps of 32 evenly, and
-// each wave issues the loads of up to CH steps before their MFMAs
-// (v_mfma_f32_16x16x32_bf16, operands read straight from memory: the weights
-// once, the few activation rows from L2).  The partial tiles are added in
-// wave order through LDS.  MB = 16-row blocks the kernel is built for (the
+// longer one in the reference's shapes: the faster counts measured) split
+// the K steps of 32 evenly, and each wave issues the loads of up to CH steps
+// before their MFMAs (v_mfma_f32_16x16x32_bf16, operands read straight from
+// memory: the weights once, the few activation rows from L2).  The partial
+// tiles are added in wave order through LDS.  MB = 16-row blocks the kernel is built for (the
 // host picks it from a bound on the group sizes; with MB > 2 fewer K steps
 // are in flight, the activation fragments take the registers).  Rows past a
 // group's end repeat its last row and are not stored.
