@@ -160,14 +160,15 @@ __global__ __launch_bounds__(256) void dispatch_gather_kernel(
   x_perm[g] = x[(slot / k) * chunks + c];
 }
 
-// Decode-sized batches (n_slots <= kSmallSlots): the four stages in one
-// launch.  Every workgroup ranks all the slots (one per thread, the ballot
-// ranking of dispatch_scatter_kernel over the block's waves) and so knows the
-// whole permutation; workgroup 0 writes counts, offsets, perm and
+// Decode-sized batches (n_slots <= kSmallSlots, dim <= 2048): the four stages
+// in one launch.  Every workgroup ranks all the slots (one per thread, the
+// ballot ranking of dispatch_scatter_kernel over the block's waves) and so
+// knows the whole permutation; workgroup 0 writes counts, offsets, perm and
 // pos_of_slot, and workgroup b copies rows kSmallRowsPerBlock * b .. + that
 // many of x_perm.  Same counting sort, same output.
 constexpr int kSmallSlots = kDispThreads;
-constexpr int kSmallRowsPerBlock = 16;
+constexpr int kSmallRowsPerBlock = 8;
+constexpr int kSmallCopies = 8;  // 16-byte copies per thread, all loads issued first (dim <= 2048)
 
 __global__ __launch_bounds__(kDispThreads) void dispatch_small_kernel(
     const int32_t* __restrict__ idx, int n_slots, int E, int k, const uint4* __restrict__ x, int chunks,
@@ -225,9 +226,20 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_small_kernel(
   __syncthreads();
   const int r0 = blockIdx.x * kSmallRowsPerBlock;
   const int r1 = min(r0 + kSmallRowsPerBlock, start[E]);  // rows that hold a slot
-  for (int g = r0 * chunks + threadIdx.x; g < r1 * chunks; g += blockDim.x) {
-    const int r = g / chunks, c = g - r * chunks;
-    x_perm[static_cast<int64_t>(r) * chunks + c] = x[static_cast<int64_t>(perm_sh[r] / k) * chunks + c];
+  const int g0 = r0 * chunks + threadIdx.x, g1 = r1 * chunks;
+  uint4 v[kSmallCopies];
+#pragma unroll
+  for (int u = 0; u < kSmallCopies; ++u) {
+    const int g = g0 + u * kDispThreads;
+    if (g < g1) {
+      const int r = g / chunks, c = g - r * chunks;
+      v[u] = x[static_cast<int64_t>(perm_sh[r] / k) * chunks + c];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kSmallCopies; ++u) {
+    const int g = g0 + u * kDispThreads;
+    if (g < g1) x_perm[g] = v[u];
   }
 }
 
@@ -261,7 +273,7 @@ extern "C" int fmoe_dispatch(const int32_t* idx, const void* x, int64_t T, int64
   if (!idx || !x || !perm || !pos_of_slot || !workspace) return FMOE_ERR_INVALID_ARG;
   if (workspace_bytes < fmoe_dispatch_workspace_bytes(T, n_experts, k)) return FMOE_ERR_WORKSPACE;
   if (!aligned16(x) || (x_perm && !aligned16(x_perm))) return FMOE_ERR_ALIGN;
-  if (n_slots <= kSmallSlots) {
+  if (n_slots <= kSmallSlots && kSmallRowsPerBlock * (dim / 8) <= kSmallCopies * kDispThreads) {
     const int chunks = static_cast<int>(dim / 8);
     const int64_t blocks = x_perm ? ceil_div(n_slots, kSmallRowsPerBlock) : 1;
     dispatch_small_kernel<<<dim3(blocks), dim3(kDispThreads), 0, s>>>(

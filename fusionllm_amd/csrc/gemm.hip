@@ -61,6 +61,7 @@ struct GemmArgs {
   const uint16_t* b0[FMOE_MAX_EXPERTS + 1];  // w1 / w2 / w2t / w13t
   const uint16_t* b1[FMOE_MAX_EXPERTS + 1];  // w3 (GATEUP_FWD only)
   int small_max;  // groups with 1 .. small_max rows go to small_gemm_kernel (0: none)
+  int small_compact;  // DOWN_FWD small kernel: the grid covers only groups with rows
   float* split_ws;  // DOWN_FWD / GATEUP_BWD: fp32 partials of K-split tiles (nullptr: no split)
 };
 
@@ -545,16 +546,47 @@ __global__ __launch_bounds__(small_waves<MODE>() * 64) void small_gemm_kernel(co
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ncb = args.N / 16;
-  const int g = blockIdx.x / ncb, cb = blockIdx.x % ncb;
-  int row_base, M;
-  if (g < args.E) {
-    row_base = args.offsets[g];
-    M = args.offsets[g + 1] - row_base;
+  const int cb = blockIdx.x % ncb;
+  int g, row_base, M;
+  if (MODE == DOWN_FWD && args.small_compact) {
+    // Fewer routed rows than experts: workgroup -> (group, column block) over
+    // the groups this kernel takes (1 .. small_max rows: routed experts in
+    // order, then the shared expert), so that the grid holds no workgroups
+    // of empty experts (empty 8-wave workgroups ahead of the busy ones cost
+    // up to 2 us at M = 1).  Lane e < E reads expert e's rows, the wave ranks
+    // the qualifying experts with a ballot and takes the rank-th.
+    const int rank = blockIdx.x / ncb, lane_e = threadIdx.x & 63;
+    int lo = 0, m_e = 0;
+    if (lane_e < args.E) {
+      lo = args.offsets[lane_e];
+      m_e = args.offsets[lane_e + 1] - lo;
+    }
+    const bool qual = m_e > 0 && m_e <= args.small_max;
+    const uint64_t qmask = __ballot(qual);
+    const int nq = __popcll(qmask);
+    if (rank < nq) {
+      const uint64_t below = lane_e == 0 ? 0ull : (qmask & (~0ull >> (64 - lane_e)));
+      g = __ffsll(static_cast<unsigned long long>(__ballot(qual && __popcll(below) == rank))) - 1;
+      row_base = __shfl(lo, g, 64);
+      M = __shfl(m_e, g, 64);
+    } else {
+      if (rank != nq || args.rows_shared == 0 || args.rows_shared > args.small_max) return;
+      g = args.E;
+      row_base = args.rows_routed;
+      M = args.rows_shared;
+    }
   } else {
-    row_base = args.rows_routed;
-    M = args.rows_shared;
+    // one workgroup per (group, column block); empty groups return at once
+    g = blockIdx.x / ncb;
+    if (g < args.E) {
+      row_base = args.offsets[g];
+      M = args.offsets[g + 1] - row_base;
+    } else {
+      row_base = args.rows_routed;
+      M = args.rows_shared;
+    }
+    if (M == 0 || M > args.small_max) return;
   }
-  if (M == 0 || M > args.small_max) return;
   const uint16_t* A = (g < args.E || args.a_shared == nullptr)
                           ? args.a_routed + static_cast<int64_t>(row_base) * args.lda
                           : args.a_shared;
@@ -990,7 +1022,11 @@ int launch_rows(GemmArgs& a, int64_t rows_routed, int64_t rows_shared, int E, vo
   }
   if constexpr (kHasSmall) {
     if (a.small_max > 0) {
-      const int G = E + (rows_shared > 0 ? 1 : 0);
+      // DOWN_FWD with fewer routed rows than experts: the grid covers the
+      // at most rows_routed routed groups that have rows
+      a.small_compact = (MODE == DOWN_FWD && rows_routed < E) ? 1 : 0;
+      const int64_t Gr = a.small_compact ? rows_routed : E;
+      const int64_t G = Gr + (rows_shared > 0 ? 1 : 0);
       const dim3 grid(G * (a.N / 16)), block(small_waves<MODE>() * 64);
       hipStream_t s = as_stream(stream);
       switch (small_blocks(rows_routed > rows_shared ? rows_routed : rows_shared)) {

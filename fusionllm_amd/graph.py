@@ -51,6 +51,12 @@ class DecodeGraph:
         if x.shape != self.x.shape or x.dtype != self.x.dtype:
             raise ValueError(f"captured for {tuple(self.x.shape)} {self.x.dtype}, got {tuple(x.shape)} {x.dtype}")
         self.x.copy_(x)
+        return self.replay()
+
+    def replay(self) -> torch.Tensor:
+        """Replay on the current contents of ``self.x`` (for callers that
+        write the tokens into the captured input in place, which saves the
+        copy of ``__call__``)."""
         self.graph.replay()
         m = self.module
         m._last_indices, m._last_weights = self.last_indices, self.last_weights

@@ -32,3 +32,16 @@ def test_decode_graph_replays_match_eager(gpu_device, cfg):
         assert torch.equal(idx, m._last_indices) and torch.equal(w.view(torch.int32), m._last_weights.view(torch.int32))
         z = torch.full((1024,), float(rep), device=gpu_device).sum()  # unrelated eager kernels
         assert float(z) == 1024.0 * rep
+
+
+def test_decode_graph_replay_in_place(gpu_device):
+    cfg = configs.C3[1]
+    data = configs.make_block(cfg, seed=2)
+    m = build_module(cfg, data, gpu_device)
+    g = DecodeGraph(m, data.x.to(gpu_device, torch.bfloat16))
+    x = (torch.randn(data.x.shape, generator=torch.Generator().manual_seed(9)) * 3).to(gpu_device, torch.bfloat16)
+    g.x.copy_(x)  # the caller writes the tokens into the captured input
+    y = g.replay().clone()
+    with torch.no_grad():
+        want = m(x)
+    assert torch.equal(y.view(torch.int16), want.view(torch.int16))

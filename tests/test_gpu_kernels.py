@@ -76,6 +76,20 @@ def test_dispatch_bit_exact(gpu_device, T, d, E, k):
     assert torch.equal(x_perm.cpu().view(torch.int16), x[rp.long() // k].view(torch.int16))
 
 
+@pytest.mark.parametrize("T,d,E,k", [(5, 4096, 8, 2), (100, 2048, 8, 2), (100, 2112, 8, 2)])
+def test_dispatch_given_indices(gpu_device, T, d, E, k):
+    # indices chosen here (no router: it takes dim <= 2048), around the row
+    # width up to which tiny batches use the one-launch dispatch
+    g = torch.Generator().manual_seed(T + d)
+    idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(torch.int32)
+    x = torch.randn(T, d, generator=g).bfloat16()
+    counts, offsets, perm, pos, x_perm = K.dispatch(idx.to(gpu_device), x.to(gpu_device), E)
+    rc, ro, rp, rpos = mo.dispatch_c(idx, E)
+    assert torch.equal(counts.cpu(), rc) and torch.equal(offsets.cpu(), ro)
+    assert torch.equal(perm.cpu(), rp) and torch.equal(pos.cpu(), rpos)
+    assert torch.equal(x_perm.cpu().view(torch.int16), x[rp.long() // k].view(torch.int16))
+
+
 @pytest.mark.parametrize("T", [5000, 200])
 def test_dispatch_all_on_one_expert(gpu_device, T):
     d, E, k = 64, 8, 1
