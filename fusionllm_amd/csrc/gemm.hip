@@ -936,12 +936,23 @@ __global__ __launch_bounds__(core::NT, 1) void wgrad_tr_kernel(const WgradArgs a
 }
 
 // Adds the chunk partials of each multi-chunk group in chunk order; 8
-// consecutive outputs per thread (m_out * n_out is a multiple of 64).
+// consecutive outputs per thread (m_out * n_out is a multiple of 64).  A
+// group without rows gets a zero gradient (no work unit of the product
+// kernel writes it).
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const WgradArgs args) {
   const int g = blockIdx.y;
   int row_base, M;
   group_rows(args, g, row_base, M);
   const int chunks = (M + args.kc - 1) / args.kc;
+  if (chunks == 0) {
+    const int64_t mn = static_cast<int64_t>(args.m_out) * args.n_out;
+    const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+    if (i0 >= mn) return;
+    const int m = static_cast<int>(i0 / args.n_out), n = static_cast<int>(i0 % args.n_out);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) store_grad(args, g, m, n + e, 0.0f);
+    return;
+  }
   if (chunks <= 1) return;
   int pbase = 0;
   for (int q = 0; q < g; ++q) {

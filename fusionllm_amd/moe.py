@@ -147,6 +147,9 @@ class SwiGLUExpert(nn.Module):
         self.w3 = nn.Linear(dim, inter_dim, bias=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if torch.compiler.is_compiling():
+            # traced: the reference's expression (models/moe.py:21), left to the compiler
+            return self.w2(F.silu(self.w1(x)) * self.w3(x))
         return dense_swiglu(x, self.w1.weight, self.w3.weight, self.w2.weight)
 
 
@@ -204,7 +207,9 @@ def _backward_pass(ctx, saved, dy):
     """Backward kernels of the MoE (autograd of models/moe.py:44-87) up to,
     not including, the per-token input-gradient reduction.  Returns
     (dx_rows, d_logits, dgw, dgb, grads_w) with grads_w per weight, None
-    for experts that got no tokens."""
+    for experts that got no tokens when ctx carries the forward's host copy
+    of the expert counts (ctx.counts_host / counts_event), zeros otherwise.
+    ctx needs .meta and .param_dtypes."""
     E, k, inter, rs, has_shared, out_dtype = ctx.meta
     xb, gwb, idx, w, v, offsets, perm, pos, x_perm, ab, h, o, *wb = saved
     T, d = xb.shape
@@ -235,11 +240,15 @@ def _backward_pass(ctx, saved, dy):
     if dgb.dtype != gb_dtype:
         dgb = dgb.to(gb_dtype)
 
-    ctx.counts_event.synchronize()
-    counts = ctx.counts_host.tolist()
     grads_w = [None] * len(wb)
+    counts = None
+    if getattr(ctx, "counts_host", None) is not None:
+        ctx.counts_event.synchronize()
+        counts = ctx.counts_host.tolist()
+    # Without the host copy of the counts (the graph-capturable operator)
+    # every expert gets its gradient: zeros for experts without rows.
     for g in range(G):
-        if g < E and counts[g] == 0:
+        if counts is not None and g < E and counts[g] == 0:
             continue
         grads_w[3 * g], grads_w[3 * g + 1], grads_w[3 * g + 2] = dw1[g], dw3[g], dw2[g]
     return dx_rows, d_logits, dgw, dgb, grads_w
@@ -404,13 +413,23 @@ class DeepSeekMoE(nn.Module):
             raise RuntimeError("the RMSNorm weight must be on the input's device")
         weights = self._flat_weights()
         out_dtype = self._output_dtype(flat, weights)
-        if flat.shape[0] == 0:
-            return x + self.forward(norm(x))  # zero tokens: empty tensors only
+        if flat.shape[0] == 0 or torch.compiler.is_compiling():
+            # zero tokens (empty tensors only), or traced: the plain expression
+            # around the block's operator
+            return x + self.forward(norm(x))
         eps = norm.eps if norm.eps is not None else torch.finfo(flat.dtype).eps
         return self._run(flat, weights, out_dtype, norm_w=nw, eps=float(eps), fused_norm=True).view(shape)
 
     def _run(self, flat, weights, out_dtype, norm_w=None, eps=0.0, fused_norm=False):
         E, k = self.n_routed_experts, self.n_activated_experts
+        if torch.compiler.is_compiling():
+            # traced (torch.compile): the block as the fusionllm::moe_fwd operator
+            y, idx64, w, counts = torch.ops.fusionllm.moe_fwd(
+                flat, self.gate.weight, self.gate.bias, weights, k, float(self.route_scale),
+                self.shared_expert is not None, out_dtype)[:4]
+            self._last_indices, self._last_weights = idx64, w
+            self._last_counts, self._counts_of = counts, idx64
+            return y
         meta = (E, k, self.moe_inter_dim, float(self.route_scale), self.shared_expert is not None, out_dtype)
         needs_grad = torch.is_grad_enabled() and (
             flat.requires_grad or self.gate.weight.requires_grad or self.gate.bias.requires_grad

@@ -201,8 +201,10 @@ int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int n_experts,
  * For w2: A = d_out, B = h, m_split = m_out = dim.  For w1/w3: A = d_ab,
  * B = x, m_split = inter (out_lo = dw1, out_hi = dw3).
  * The reduction over rows is split into fixed chunks summed in chunk order,
- * so the result is deterministic.  Experts with no rows are left untouched
- * (the reference leaves their .grad as None, moe.py:66-72). */
+ * so the result is deterministic.  Experts with no rows get a zero G_e
+ * (the module still reports None for them, as the reference leaves their
+ * .grad unset, moe.py:66-72; the graph-capturable operator returns the
+ * zeros).  With rows_routed + rows_shared == 0 nothing is written. */
 size_t fmoe_weight_grad_workspace_bytes(int64_t rows_routed, int64_t rows_shared,
                                         int n_experts, int64_t m_out, int64_t n_out);
 int fmoe_weight_grad(const void* a_routed, const void* a_shared, int64_t lda,

@@ -203,3 +203,31 @@ def test_checkpoint_round_trip_keeps_reference_layout(tmp_path):
     for k, v in b.state_dict().items():
         assert torch.equal(v, state[k].float()), k
     assert sorted(state) == sorted(dict(a.named_parameters()))
+
+
+def test_operator_fake_shapes():
+    # The fusionllm::moe_fwd / moe_bwd operators under fake tensors (what
+    # torch.compile traces with): static output shapes and dtypes, no kernel
+    # call, no GPU needed.
+    import fusionllm_amd  # noqa: F401  (registers the operators)
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    T, d, E, k, inter = 5, 64, 4, 2, 128
+    with FakeTensorMode():
+        bf = dict(device="cuda", dtype=torch.bfloat16)
+        x = torch.empty(T, d, device="cuda", dtype=torch.float32)
+        gw, gb = torch.empty(E, d, **bf), torch.empty(E, **bf)
+        ws = []
+        for _ in range(E + 1):
+            ws += [torch.empty(inter, d, **bf), torch.empty(inter, d, **bf), torch.empty(d, inter, **bf)]
+        out = torch.ops.fusionllm.moe_fwd(x, gw, gb, ws, k, 1.0, True, torch.float32)
+        rows = T * k + T
+        assert [tuple(o.shape) for o in out] == [
+            (T, d), (T, k), (T, k), (E,), (T, k), (T, k), (E + 1,), (T * k,), (T * k,), (T * k, d),
+            (rows, 2 * inter), (rows, inter), (rows, d)]
+        assert [o.dtype for o in out[:4]] == [torch.float32, torch.int64, torch.float32, torch.int32]
+        y, idx64, w, counts, idx, v, offsets, perm, pos, x_perm, ab, h, o = out
+        g = torch.ops.fusionllm.moe_bwd(y, x, gw, gb, ws, idx, w, v, offsets, perm, pos, x_perm, ab, h, o,
+                                        k, 1.0, True)
+        assert len(g) == 3 + len(ws)
+        assert (tuple(g[0].shape), g[0].dtype) == ((T, d), torch.float32)
+        assert all(tuple(a.shape) == tuple(b.shape) for a, b in zip(g[3:], ws))
