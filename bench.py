@@ -46,7 +46,10 @@ def parse():
     p.add_argument("--config", default="C2-bf16-fwdbwd-skewed",
                    help="workload name from fusionllm_amd.configs, or its prefix C1..C5")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-tokens", type=int, default=2048, help="token sample for the CPU baseline")
+    p.add_argument("--cpu-tokens", type=int, default=4096,
+                   help="tokens per CPU-baseline pass (passes repeat for --cpu-seconds)")
+    p.add_argument("--cpu-seconds", type=float, default=12.0,
+                   help="CPU work the baseline sample is sized to (repeated passes, at least 3)")
     p.add_argument("--fwd-only", action="store_true",
                    help="time the forward pass alone (decode-shaped C3 configs); not the headline metric")
     p.add_argument("--graph", action="store_true",
@@ -187,11 +190,14 @@ def hbm_traffic(cfg_name, entry):
     return round(sum((k["FETCH_SIZE_KiB"] * fs + k["WRITE_SIZE_KiB"] * ws) * 1024.0 for k in ks))
 
 
-def cpu_baseline(cfg, data, n_tokens):
+def cpu_baseline(cfg, data, n_tokens, seconds=12.0):
     """Reference algorithm on host cores: the oracle's torch-CPU restatement of
-    models/moe.py, bf16, forward + backward, on the first n_tokens tokens."""
+    models/moe.py, bf16, forward + backward, on the first n_tokens tokens,
+    repeated until about `seconds` of CPU work (at least 3 passes, at most
+    2.5x that time); value = tokens processed / time of the timed passes."""
     from oracle import moe_oracle as mo
-    torch.set_num_threads(os.cpu_count() or 1)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count() or 1
+    torch.set_num_threads(threads)
     T = min(n_tokens, data.x.shape[0])
     sd = {k: v.bfloat16().clone().requires_grad_(True) for k, v in data.state_dict().items()}
     E = cfg.n_experts
@@ -219,23 +225,20 @@ def cpu_baseline(cfg, data, n_tokens):
 
     step()  # warmup
     times = []
-    budget = time.perf_counter() + 30.0
-    for _ in range(3):
+    t_start = time.perf_counter()
+    while len(times) < 3 or (sum(times) < seconds and time.perf_counter() - t_start < 2.5 * seconds):
         t0 = time.perf_counter()
         step()
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() > budget:
-            break
-    med = statistics.median(times)
     return {
-        "value": T / med,
+        "value": T * len(times) / sum(times),
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": (f"{cfg.name}: first {T} of {cfg.tokens} tokens"
                    + (f", {cfg.layers} x (RMSNorm + MoE + residual)" if cfg.layers > 1 else "")
                    + f", reference module semantics (bf16 router), bf16 forward+backward in torch CPU, "
-                   f"median of {len(times)} after 1 warmup"),
+                   f"{len(times)} passes ({sum(times):.1f} s) after 1 warmup"),
     }
 
 
@@ -489,7 +492,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline and not args.fwd_only:
-        cpu = cpu_baseline(cfg, data, args.cpu_tokens)
+        cpu = cpu_baseline(cfg, data, args.cpu_tokens, args.cpu_seconds)
 
     line = {
         "metric": (METRIC if cfg.layers == 1 else
