@@ -18,7 +18,7 @@ namespace fmoe {
 
 constexpr int kRouterLanes = 16;
 constexpr int kRouterTok = 32;       // tokens per workgroup (32 x 16 lanes = 512 threads)
-constexpr int kRouterEBlk = 16;      // experts whose gate rows sit in LDS at a time
+constexpr int kRouterEBlk = 8;       // experts whose gate rows sit in LDS at a time (fp32: 64 KB at dim 2048)
 constexpr int kRouterMaxDim = 2048;  // a lane keeps its <= 16 x chunks in registers
 
 // One workgroup routes 32 tokens.  The gate rows are staged in LDS, 16
@@ -86,7 +86,11 @@ __global__ __launch_bounds__(512) void router_fwd_kernel(
     int32_t* __restrict__ idx, int64_t* __restrict__ idx64, float* __restrict__ wout,
     float* __restrict__ vout) {
   constexpr int EBLK = EB < kRouterEBlk ? EB : kRouterEBlk;  // experts per LDS block
-  __shared__ __attribute__((aligned(16))) uint4 wsh[EBLK * NQ * kRouterLanes];
+  // Gate rows converted to fp32 once per workgroup, each 8-element chunk as
+  // two float4 planes (elements 0-3, 4-7): consecutive lanes read consecutive
+  // 16-byte words, and no lane unpacks bf16 per token.
+  __shared__ float4 wlo[EBLK * NQ * kRouterLanes];
+  __shared__ float4 whi[EBLK * NQ * kRouterLanes];
   __shared__ float lsh[kRouterTok * EB];
   const int lane16 = threadIdx.x % kRouterLanes;
   const int tl = threadIdx.x / kRouterLanes;
@@ -106,8 +110,12 @@ __global__ __launch_bounds__(512) void router_fwd_kernel(
   for (int e0 = 0; e0 < E; e0 += EBLK) {
     const int ne = min(EBLK, E - e0);
     __syncthreads();  // the previous block's gate rows are no longer read
-    for (int i = threadIdx.x; i < ne * nchunk; i += blockDim.x)
-      wsh[i] = reinterpret_cast<const uint4*>(wg + static_cast<int64_t>(e0) * dim)[i];
+    for (int i = threadIdx.x; i < ne * nchunk; i += blockDim.x) {
+      float f[8];
+      unpack8(reinterpret_cast<const uint4*>(wg + static_cast<int64_t>(e0) * dim)[i], f);
+      wlo[i] = make_float4(f[0], f[1], f[2], f[3]);
+      whi[i] = make_float4(f[4], f[5], f[6], f[7]);
+    }
     __syncthreads();
     float acc[EBLK];
 #pragma unroll
@@ -121,8 +129,8 @@ __global__ __launch_bounds__(512) void router_fwd_kernel(
 #pragma unroll
         for (int e = 0; e < EBLK; ++e) {
           if (e < ne) {
-            float wf[8];
-            unpack8(wsh[e * nchunk + c], wf);
+            const float4 a = wlo[e * nchunk + c], b = whi[e * nchunk + c];
+            const float wf[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
             for (int i = 0; i < 8; ++i) acc[e] = fmaf(xf[i], wf[i], acc[e]);
           }
