@@ -52,6 +52,8 @@ def parse():
                    help="CPU work the baseline sample is sized to (repeated passes, at least 3)")
     p.add_argument("--fwd-only", action="store_true",
                    help="time the forward pass alone (decode-shaped C3 configs); not the headline metric")
+    p.add_argument("--autocast", action="store_true",
+                   help="fp32 module and input under bf16 autocast (the trainer's setting); single block")
     p.add_argument("--graph", action="store_true",
                    help="with --fwd-only: time HIP-graph replays of the forward (DecodeGraph)")
     p.add_argument("--optimizer", action="store_true",
@@ -341,10 +343,14 @@ def main():
     torch.cuda.set_device(dev)
     data = configs.make_block(cfg, seed=0)
 
+    # --autocast: the trainer's setting (training/trainer.py:158), fp32
+    # parameters and activations under bf16 autocast; default: a bf16 module.
+    pdt = torch.float32 if args.autocast else torch.bfloat16
+
     def module(d):
         m = DeepSeekMoE(cfg.moe_config())
-        m.load_state_dict({k: v.bfloat16() for k, v in d.state_dict().items()})
-        return m.to(device=dev, dtype=torch.bfloat16)
+        m.load_state_dict({k: v.to(pdt) for k, v in d.state_dict().items()})
+        return m.to(device=dev, dtype=pdt)
 
     # C4: a stack of cfg.layers blocks x + MoE(RMSNorm(x)) (models/fusionllm.py:48,52),
     # independent seeded weights per layer, norm weights ones (their init).
@@ -352,11 +358,16 @@ def main():
                              for l in range(1, cfg.layers)]
     norms = [torch.nn.RMSNorm(cfg.dim, eps=1e-6).to(device=dev, dtype=torch.bfloat16)
              for _ in range(cfg.layers)] if cfg.layers > 1 else []
-    x = data.x.to(dev, torch.bfloat16).requires_grad_(True)
-    dy = data.dy.to(dev, torch.bfloat16)
+    x = data.x.to(dev, pdt).requires_grad_(True)
+    dy = data.dy.to(dev, pdt)
+    if args.autocast and norms:
+        raise SystemExit("--autocast times the single block (C1..C3, C5)")
     T = x.shape[0]
 
     def forward():
+        if args.autocast:
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                return mods[0](x)
         if not norms:
             return mods[0](x)
         h = x
@@ -513,7 +524,8 @@ def main():
                    "experts": cfg.n_experts, "topk": cfg.topk, "shared": int(cfg.n_shared > 0),
                    "bias": cfg.bias, "layers": cfg.layers,
                    "pass": "forward" if args.fwd_only else "forward+backward",
-                   "launch": "hip-graph replay" if args.graph else "eager"},
+                   "launch": "hip-graph replay" if args.graph else "eager",
+                   "params": "fp32 under bf16 autocast" if args.autocast else "bf16"},
         "grouped_gemm_mfma_frac": round(gemm_flops / gemm_s / PEAK_BF16_FLOPS, 4),
         "step_mfma_frac": round(gemm_flops / (elapsed / args.steps) / PEAK_BF16_FLOPS, 4),
         "roofline": roofline,

@@ -369,3 +369,23 @@ def normuon_step(params, grads, exp_avgs, exp_avg_sqs, lr: float, beta1: float, 
                                 float(lr), float(beta1), float(beta2), float(eps), float(weight_decay),
                                 int(bool(cautious)), float(bias_corr1), float(bias_corr2), _stream()),
           "fmoe_normuon_step")
+
+
+CAST_MAX_TENSORS = 64
+
+
+def cast_bf16(tensors):
+    """bf16 copies of contiguous fp32 device tensors, one launch per 64
+    (round to nearest even, bit-identical to .to(torch.bfloat16))."""
+    lib = _lib.load()
+    outs = []
+    for i0 in range(0, len(tensors), CAST_MAX_TENSORS):
+        chunk = tensors[i0:i0 + CAST_MAX_TENSORS]
+        n = len(chunk)
+        dst = [torch.empty(t.shape, dtype=torch.bfloat16, device=t.device) for t in chunk]
+        src_p = (ctypes.c_void_p * n)(*[_req(t, "cast source", torch.float32) for t in chunk])
+        dst_p = (ctypes.c_void_p * n)(*[d.data_ptr() for d in dst])
+        cnt = (ctypes.c_int64 * n)(*[t.numel() for t in chunk])
+        check(lib.fmoe_cast_bf16(src_p, dst_p, cnt, n, _stream()), "fmoe_cast_bf16")
+        outs += dst
+    return outs

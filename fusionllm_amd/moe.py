@@ -40,6 +40,25 @@ def _as_bf16(t: torch.Tensor) -> torch.Tensor:
     return t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)
 
 
+def _bf16_operands(ts: list) -> list:
+    """Contiguous bf16 versions of the block's operands: bf16 ones as they
+    are, contiguous fp32 ones converted together in one launch (the casts
+    autocast would make one nn.Linear at a time), anything else by .to()."""
+    out = list(ts)
+    idx = []
+    for i, t in enumerate(ts):
+        if t.dtype == torch.bfloat16:
+            out[i] = t.contiguous()
+        elif t.dtype == torch.float32 and t.is_contiguous() and t.data_ptr() % 16 == 0:
+            idx.append(i)
+        else:
+            out[i] = t.to(torch.bfloat16).contiguous()
+    if idx:
+        for i, c in zip(idx, K.cast_bf16([ts[i] for i in idx])):
+            out[i] = c
+    return out
+
+
 _DENSE_OFFSETS: dict = {}
 
 
@@ -67,8 +86,7 @@ class _DenseSwiGLUFunction(torch.autograd.Function):
     def forward(ctx, x, w1, w3, w2):
         T, d = x.shape
         inter = w1.shape[0]
-        xb = _as_bf16(x).contiguous()
-        w1b, w3b, w2b = (_as_bf16(w).contiguous() for w in (w1, w3, w2))
+        xb, w1b, w3b, w2b = _bf16_operands([x, w1, w3, w2])
         off = _dense_offsets(T, x.device)
         ab, h = K.gateup_fwd(xb, None, off, 1, [w1b], [w3b], inter)
         y = K.down_fwd(h, off, 1, T, 0, [w2b], d)
@@ -165,9 +183,7 @@ def _forward_pass(meta, x, gate_w, gate_b, weights, residual=None):
     residual the output is residual + moe(x) (models/fusionllm.py:52)."""
     E, k, inter, rs, has_shared, out_dtype = meta
     T, d = x.shape
-    xb = _as_bf16(x).contiguous()
-    gwb, gbb = _as_bf16(gate_w).contiguous(), _as_bf16(gate_b).contiguous()
-    wb = [_as_bf16(w).contiguous() for w in weights]
+    xb, gwb, gbb, *wb = _bf16_operands([x, gate_w, gate_b, *weights])
     G = E + (1 if has_shared else 0)
     w1s, w3s, w2s = wb[0::3][:G], wb[1::3][:G], wb[2::3][:G]
 

@@ -26,7 +26,7 @@ import torch
 from torch import Tensor
 
 from . import _kernels as K
-from .moe import _as_bf16, _backward_pass, _forward_pass
+from .moe import _backward_pass, _bf16_operands, _forward_pass
 
 
 def _meta(gate_w: Tensor, weights: list[Tensor], k: int, route_scale: float, has_shared: bool,
@@ -63,9 +63,7 @@ def moe_bwd(dy: Tensor, x: Tensor, gate_w: Tensor, gate_b: Tensor, weights: list
             w: Tensor, v: Tensor, offsets: Tensor, perm: Tensor, pos: Tensor, x_perm: Tensor, ab: Tensor,
             h: Tensor, o: Tensor, k: int, route_scale: float, has_shared: bool) -> list[Tensor]:
     meta = _meta(gate_w, weights, k, route_scale, has_shared, dy.dtype)
-    xb = _as_bf16(x).contiguous()
-    gwb = _as_bf16(gate_w).contiguous()
-    wb = [_as_bf16(t).contiguous() for t in weights]
+    xb, gwb, *wb = _bf16_operands([x, gate_w, *weights])
     ctx = types.SimpleNamespace(meta=meta, param_dtypes=(gate_w.dtype, gate_b.dtype, [t.dtype for t in weights]))
     saved = (xb, gwb, idx, w, v, offsets, perm, pos, x_perm, ab, h, o, *wb)
     dx_rows, d_logits, dgw, dgb, grads_w = _backward_pass(ctx, saved, dy.contiguous())

@@ -41,9 +41,10 @@
 extern "C" {
 #endif
 
-#define FMOE_ABI_VERSION 5
+#define FMOE_ABI_VERSION 6
 #define FMOE_MAX_EXPERTS 64
 #define FMOE_MAX_TOPK 8
+#define FMOE_MAX_CAST 64
 
 enum fmoe_status {
   FMOE_OK = 0,
@@ -299,6 +300,18 @@ int fmoe_normuon_step(void* const* params, const void* const* grads,
                       double lr, double beta1, double beta2, double eps,
                       double weight_decay, int cautious, double bias_corr1,
                       double bias_corr2, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * bf16 copies of up to FMOE_MAX_CAST fp32 tensors in one launch.  Under the
+ * trainer's bf16 autocast (training/trainer.py:158) each nn.Linear of the
+ * block casts its fp32 weight to bf16 (models/moe.py:16-18, the gate at
+ * moe.py:36,46), one cast per weight; this replaces those casts (and the
+ * input's) for the whole block.  dst[i] = bf16(src[i]) for n[i] elements,
+ * round to nearest even as torch's .to(torch.bfloat16); src and dst 16-byte
+ * aligned, contiguous.
+ * ------------------------------------------------------------------------- */
+int fmoe_cast_bf16(const void* const* src, void* const* dst, const int64_t* n,
+                   int n_tensors, void* stream);
 
 #ifdef __cplusplus
 }

@@ -223,3 +223,26 @@ def test_transpose_weights_bit_exact(gpu_device, G, d, I):
     want2 = torch.stack([w.T for w in w2])
     assert torch.equal(w13t.cpu().view(torch.int16), want13.contiguous().view(torch.int16))
     assert torch.equal(w2t.cpu().view(torch.int16), want2.contiguous().view(torch.int16))
+
+
+def test_cast_bf16_bit_exact(gpu_device):
+    # One-launch fp32 -> bf16 copies (the autocast casts of the block's
+    # operands): bit-identical to torch's .to(torch.bfloat16), round to
+    # nearest even, tails shorter than 8 values, more tensors than one launch
+    # takes, special values.
+    g = torch.Generator().manual_seed(0)
+    sizes = [0, 1, 7, 8, 9, 2047, 2048, 2049, 100003] + [64] * 60
+    ts = [torch.randn(n, generator=g) * 10 for n in sizes]
+    ts.append(torch.tensor([float("inf"), -float("inf"), 0.0, -0.0, 1e-40, -1e-40, 3.4e38, -3.4e38,
+                            1.00390625, 1.01171875, -1.00390625, 2.0 ** -126, 2.0 ** -133, 65504.0,
+                            3.3895313892515355e38, float("nan")]))
+    ts.append(torch.randn(3, 5, generator=g))  # 2-D, 15 values
+    out = K.cast_bf16([t.to(gpu_device) for t in ts])
+    assert len(out) == len(ts)
+    for t, o in zip(ts, out):
+        want = t.to(torch.bfloat16)
+        got = o.cpu()
+        assert got.shape == want.shape and got.dtype == torch.bfloat16
+        nan = torch.isnan(want)
+        assert torch.equal(torch.isnan(got), nan)
+        assert torch.equal(got[~nan].view(torch.int16), want[~nan].view(torch.int16))

@@ -21,7 +21,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     syms = declared_symbols()
-    assert len(syms) == 22
+    assert len(syms) == 23
     for s in syms:
         assert hasattr(lib, s), s
     assert set(syms) == set(_lib.SIGNATURES), "ctypes binding and header disagree"
@@ -37,6 +37,7 @@ def test_status_strings():
 
 
 def test_argument_errors_without_gpu():
+    import ctypes
     lib = _lib.load()
     # rejected on the host before any HIP call
     assert lib.fmoe_router_fwd(None, None, None, 4, 100, 8, 2, 1.0, None, None, None, None, None) == 2  # dim % 64
@@ -63,6 +64,13 @@ def test_argument_errors_without_gpu():
                                    None, 0, None, None, None, 0, None) == 1  # null inputs
     assert lib.fmoe_weight_grad(None, None, 8, None, None, 8, None, 1, 10, 0, 128, 128, 0, pp, None, 0,
                                 None, 0, None) == 2
+    # one-launch bf16 casts: count and sizes checked before any pointer is used
+    n1 = (ctypes.c_int64 * 1)(-1)
+    assert lib.fmoe_cast_bf16(pp, pp, n1, 1, None) == 1
+    assert lib.fmoe_cast_bf16(pp, pp, n1, 65, None) == 1
+    assert lib.fmoe_cast_bf16(None, None, None, 0, None) == 0
+    assert lib.fmoe_cast_bf16(_lib.ptr_array([fake + 4]), _lib.ptr_array([fake]), (ctypes.c_int64 * 1)(8), 1,
+                              None) == 3
     # size queries
     assert lib.fmoe_dispatch_workspace_bytes(16384, 8, 2) == 2 * 128 * 8 * 4
     assert lib.fmoe_weight_grad_workspace_bytes(32768, 16384, 8, 768, 2048) > 0
