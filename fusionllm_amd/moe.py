@@ -97,25 +97,31 @@ class _DenseSwiGLUFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         xb, ab, h, w1b, w3b, w2b, off = ctx.saved_tensors
-        x_dtype, w1_dtype, w3_dtype, w2_dtype = ctx.dtypes
-        T, d = xb.shape
-        inter = w1b.shape[0]
-        dyb = _as_bf16(dy).contiguous()
-        w13t, w2t = K.transpose_weights([w1b], [w3b], [w2b])
-        d_ab = K.down_bwd_dx(dyb, None, off, 1, w2t, ab, inter)
-        dw2 = torch.empty(d, inter, dtype=w2_dtype, device=xb.device)
-        K.weight_grad(dyb, None, h, None, off, 1, T, 0, d, [dw2], None, w2_dtype, tag="w2")
-        dx = None
-        if ctx.needs_input_grad[0]:
-            dx = K.gateup_bwd_dx(d_ab, off, 1, T, 0, w13t, d)
-            if dx.dtype != x_dtype:
-                dx = dx.to(x_dtype)
-        dw1 = torch.empty(inter, d, dtype=w1_dtype, device=xb.device)
-        dw3 = torch.empty(inter, d, dtype=w1_dtype, device=xb.device)
-        K.weight_grad(d_ab, None, xb, None, off, 1, T, 0, inter, [dw1], [dw3], w1_dtype, tag="w13")
-        if w3_dtype != w1_dtype:
-            dw3 = dw3.to(w3_dtype)
-        return dx, dw1, dw3, dw2
+        return _dense_backward(dy, xb, ab, h, w1b, w3b, w2b, off, ctx.dtypes, ctx.needs_input_grad[0])
+
+
+def _dense_backward(dy, xb, ab, h, w1b, w3b, w2b, off, dtypes, need_dx):
+    """Backward kernels of the one-group SwiGLU: (dx or None, dw1, dw3, dw2)
+    in the dtypes (x, w1, w3, w2) of dtypes."""
+    x_dtype, w1_dtype, w3_dtype, w2_dtype = dtypes
+    T, d = xb.shape
+    inter = w1b.shape[0]
+    dyb = _as_bf16(dy).contiguous()
+    w13t, w2t = K.transpose_weights([w1b], [w3b], [w2b])
+    d_ab = K.down_bwd_dx(dyb, None, off, 1, w2t, ab, inter)
+    dw2 = torch.empty(d, inter, dtype=w2_dtype, device=xb.device)
+    K.weight_grad(dyb, None, h, None, off, 1, T, 0, d, [dw2], None, w2_dtype, tag="w2")
+    dx = None
+    if need_dx:
+        dx = K.gateup_bwd_dx(d_ab, off, 1, T, 0, w13t, d)
+        if dx.dtype != x_dtype:
+            dx = dx.to(x_dtype)
+    dw1 = torch.empty(inter, d, dtype=w1_dtype, device=xb.device)
+    dw3 = torch.empty(inter, d, dtype=w1_dtype, device=xb.device)
+    K.weight_grad(d_ab, None, xb, None, off, 1, T, 0, inter, [dw1], [dw3], w1_dtype, tag="w13")
+    if w3_dtype != w1_dtype:
+        dw3 = dw3.to(w3_dtype)
+    return dx, dw1, dw3, dw2
 
 
 def dense_swiglu(x: torch.Tensor, w1: torch.Tensor, w3: torch.Tensor, w2: torch.Tensor) -> torch.Tensor:
@@ -165,10 +171,12 @@ class SwiGLUExpert(nn.Module):
         self.w3 = nn.Linear(dim, inter_dim, bias=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        w1, w3, w2 = self.w1.weight, self.w3.weight, self.w2.weight
         if torch.compiler.is_compiling():
-            # traced: the reference's expression (models/moe.py:21), left to the compiler
-            return self.w2(F.silu(self.w1(x)) * self.w3(x))
-        return dense_swiglu(x, self.w1.weight, self.w3.weight, self.w2.weight)
+            # traced (torch.compile): the fusionllm::swiglu_fwd operator
+            flat = x.reshape(-1, w1.shape[1])
+            return torch.ops.fusionllm.swiglu_fwd(flat, w1, w3, w2)[0].view(*x.shape[:-1], w2.shape[0])
+        return dense_swiglu(x, w1, w3, w2)
 
 
 class DenseFFN(SwiGLUExpert):

@@ -1,5 +1,5 @@
-"""DeepSeekMoE block as two torch.library operators, for torch.compile and
-graph capture.
+"""DeepSeekMoE block (and the dense SwiGLU) as torch.library operators, for
+torch.compile and graph capture.
 
 ``fusionllm::moe_fwd`` and ``fusionllm::moe_bwd`` run the same kernels as
 the module's eager path (models/moe.py:44-87 forward, its autograd backward)
@@ -17,6 +17,11 @@ fp32, counts [E] int32, then the tensors the backward reads: idx32 [T,k],
 topv [T,k] fp32, offsets [E+1], perm [T*k], pos_of_slot [T*k], x_perm
 [T*k,d] bf16, ab [rows,2I] bf16, h [rows,I] bf16, o [rows,d] bf16.
 moe_bwd returns [dx, d_gate_w, d_gate_b, *d_weights] in the inputs' dtypes.
+
+``fusionllm::swiglu_fwd`` / ``swiglu_bwd`` do the same for the dense SwiGLU
+(models/moe.py:11-21 used alone, the DenseFFN of models/fusionllm.py:17-27):
+outputs y [T,d] bf16, ab [T,2I] bf16, h [T,I] bf16; gradients [dx, dw1,
+dw3, dw2] in the inputs' dtypes.
 """
 from __future__ import annotations
 
@@ -26,7 +31,7 @@ import torch
 from torch import Tensor
 
 from . import _kernels as K
-from .moe import _backward_pass, _bf16_operands, _forward_pass
+from .moe import _backward_pass, _bf16_operands, _dense_backward, _dense_offsets, _forward_pass
 
 
 def _meta(gate_w: Tensor, weights: list[Tensor], k: int, route_scale: float, has_shared: bool,
@@ -97,3 +102,53 @@ def _backward(ctx, dy, *unused):
 
 
 moe_fwd.register_autograd(_backward, setup_context=_setup_context)
+
+
+@torch.library.custom_op("fusionllm::swiglu_fwd", mutates_args=())
+def swiglu_fwd(x: Tensor, w1: Tensor, w3: Tensor, w2: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    T, d = x.shape
+    inter = w1.shape[0]
+    xb, w1b, w3b, w2b = _bf16_operands([x, w1, w3, w2])
+    off = _dense_offsets(T, x.device)
+    ab, h = K.gateup_fwd(xb, None, off, 1, [w1b], [w3b], inter)
+    y = K.down_fwd(h, off, 1, T, 0, [w2b], d)
+    return y, ab, h
+
+
+@swiglu_fwd.register_fake
+def _(x, w1, w3, w2):
+    T, inter = x.shape[0], w1.shape[0]
+    bf = torch.bfloat16
+    return (x.new_empty((T, w2.shape[0]), dtype=bf), x.new_empty((T, 2 * inter), dtype=bf),
+            x.new_empty((T, inter), dtype=bf))
+
+
+@torch.library.custom_op("fusionllm::swiglu_bwd", mutates_args=())
+def swiglu_bwd(dy: Tensor, x: Tensor, w1: Tensor, w3: Tensor, w2: Tensor, ab: Tensor, h: Tensor) -> list[Tensor]:
+    xb, w1b, w3b, w2b = _bf16_operands([x, w1, w3, w2])
+    off = _dense_offsets(x.shape[0], x.device)
+    dx, dw1, dw3, dw2 = _dense_backward(dy, xb, ab, h, w1b, w3b, w2b, off,
+                                        (x.dtype, w1.dtype, w3.dtype, w2.dtype), True)
+    return [dx, dw1, dw3, dw2]
+
+
+@swiglu_bwd.register_fake
+def _(dy, x, w1, w3, w2, ab, h):
+    return [torch.empty_like(x), torch.empty_like(w1), torch.empty_like(w3), torch.empty_like(w2)]
+
+
+def _swiglu_setup(ctx, inputs, output):
+    x, w1, w3, w2 = inputs
+    y, ab, h = output
+    ctx.save_for_backward(x, w1, w3, w2, ab, h)
+
+
+def _swiglu_backward(ctx, dy, *unused):
+    x, w1, w3, w2, ab, h = ctx.saved_tensors
+    if dy is None:
+        return None, None, None, None
+    dx, dw1, dw3, dw2 = torch.ops.fusionllm.swiglu_bwd(dy, x, w1, w3, w2, ab, h)
+    return dx, dw1, dw3, dw2
+
+
+swiglu_fwd.register_autograd(_swiglu_backward, setup_context=_swiglu_setup)

@@ -107,3 +107,30 @@ def test_operator_opcheck(gpu_device):
     args = (x, m.gate.weight, m.gate.bias, m._flat_weights(), 2, 1.0, True, torch.bfloat16)
     torch.library.opcheck(torch.ops.fusionllm.moe_fwd.default, args,
                           test_utils=("test_schema", "test_faketensor", "test_autograd_registration"))
+
+
+def test_compiled_dense_ffn_matches_eager(gpu_device):
+    # DenseFFN (models/fusionllm.py:17-27) traced: the fusionllm::swiglu_fwd /
+    # swiglu_bwd operators, bit-equal to the eager module.
+    from fusionllm_amd import DenseFFN
+    torch._dynamo.reset()
+    g = torch.Generator().manual_seed(8)
+    f = DenseFFN(256, 512)
+    with torch.no_grad():
+        for p in f.parameters():
+            p.copy_(torch.randn(p.shape, generator=g) * 0.05)
+    f = f.to(gpu_device, torch.bfloat16)
+    x = torch.randn(3, 70, 256, generator=g).to(gpu_device, torch.bfloat16)
+    dy = torch.randn(3, 70, 256, generator=g).to(gpu_device, torch.bfloat16)
+
+    def run(fn):
+        f.zero_grad(set_to_none=True)
+        xx = x.clone().requires_grad_(True)
+        y = fn(xx)
+        y.backward(dy)
+        return y.detach(), xx.grad, [p.grad for p in f.parameters()]
+    y0, dx0, g0 = run(f)
+    y1, dx1, g1 = run(torch.compile(f, fullgraph=True, backend="aot_eager"))
+    assert torch.equal(_bits(y1), _bits(y0)) and torch.equal(_bits(dx1), _bits(dx0))
+    for a, b in zip(g1, g0):
+        assert torch.equal(_bits(a), _bits(b))
