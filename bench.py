@@ -94,6 +94,8 @@ def kernel_model(cfg, T, active_groups=None):
             "down_fwd": ("hbm", active_groups * d * I * 2 + rows * (I + d) * 2),
             "router_fwd": ("hbm", T * (2 * d + 4 * k + 8 * k + 4 * k + 4 * k) + E * (d + 1) * 2),
             "dispatch": ("hbm", T * (4 * k + 2 * d + k * 2 * d + 8 * k + 4 * k)),
+            "route_dispatch": ("hbm", T * (2 * d + 4 * k + 8 * k + 4 * k + 4 * k) + E * (d + 1) * 2
+                               + T * (k * 2 * d + 8 * k) + 8 * E),
             "combine_fwd": ("hbm", T * (k * 2 * d + 2 * d + 8 * k + 4 * k + 2 * d)),
         }
     return {
@@ -139,14 +141,17 @@ def graph_entry_times(m, x, reps=20, replays=20):
     w1s, w3s, w2s = wb[0::3][:G], wb[1::3][:G], wb[2::3][:G]
     gbb = m.gate.bias.to(torch.bfloat16).contiguous()
     rows_r, rows_s = T * k, (T if has_shared else 0)
-    calls = {
-        "router_fwd": lambda: K.router_fwd(xb, gwb, gbb, k, float(m.route_scale)),
-        "dispatch": lambda: K.dispatch(idx, xb, E),
+    if T <= K.TINY_BATCH and T * E <= 64:
+        calls = {"route_dispatch": lambda: K.route_dispatch(xb, gwb, gbb, k, float(m.route_scale))}
+    else:
+        calls = {"router_fwd": lambda: K.router_fwd(xb, gwb, gbb, k, float(m.route_scale)),
+                 "dispatch": lambda: K.dispatch(idx, xb, E)}
+    calls.update({
         "gateup_fwd": lambda: K.gateup_fwd(x_perm, xb if has_shared else None, offsets, E, w1s, w3s,
                                            m.moe_inter_dim),
         "down_fwd": lambda: K.down_fwd(h, offsets, E, rows_r, rows_s, w2s, d),
         "combine_fwd": lambda: K.combine_fwd(o, idx, w, pos, rows_r, has_shared, x.dtype, None),
-    }
+    })
     out = {}
     for name, fn in calls.items():
         side = torch.cuda.Stream()

@@ -92,6 +92,35 @@ def router_fwd(x, gate_w, gate_b, k: int, route_scale: float):
     return idx, idx64, w, v
 
 
+TINY_BATCH = 16  # fmoe_route_dispatch takes up to this many tokens
+
+
+@_timed
+def route_dispatch(x, gate_w, gate_b, k: int, route_scale: float):
+    """router_fwd followed by dispatch for T <= TINY_BATCH tokens, one launch;
+    returns idx32, idx64, weights, topv, counts, offsets, perm, pos, x_perm."""
+    lib = _lib.load()
+    T, d = x.shape
+    E = gate_w.shape[0]
+    dev = x.device
+    idx = torch.empty(T, k, dtype=torch.int32, device=dev)
+    idx64 = torch.empty(T, k, dtype=torch.int64, device=dev)
+    w = torch.empty(T, k, dtype=torch.float32, device=dev)
+    v = torch.empty(T, k, dtype=torch.float32, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(T * k, dtype=torch.int32, device=dev)
+    pos = torch.empty(T * k, dtype=torch.int32, device=dev)
+    x_perm = torch.empty(T * k, d, dtype=torch.bfloat16, device=dev)
+    check(lib.fmoe_route_dispatch(_req(x, "x", torch.bfloat16), _req(gate_w, "gate.weight", torch.bfloat16),
+                                  _req(gate_b, "gate.bias", torch.bfloat16), T, d, E, k, float(route_scale),
+                                  idx.data_ptr(), idx64.data_ptr(), w.data_ptr(), v.data_ptr(),
+                                  counts.data_ptr(), offsets.data_ptr(), perm.data_ptr(), pos.data_ptr(),
+                                  x_perm.data_ptr(), _stream()),
+          "fmoe_route_dispatch")
+    return idx, idx64, w, v, counts, offsets, perm, pos, x_perm
+
+
 @_timed
 def dispatch(idx, x, n_experts: int, gather: bool = True):
     """Histogram + scan + stable scatter (+ row gather); returns counts, offsets, perm, pos, x_perm."""

@@ -13,7 +13,7 @@ from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int64, c_size_
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libfusionmoe.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 MAX_EXPERTS = 64
 MAX_TOPK = 8
 
@@ -64,6 +64,8 @@ SIGNATURES = {
                                   c_int, c_int, c_double, c_double, c_double, c_double, c_double, c_int,
                                   c_double, c_double, _P]),
     "fmoe_cast_bf16": (c_int, [_PP, _PP, POINTER(c_int64), c_int, _P]),
+    "fmoe_route_dispatch": (c_int, [_P, _P, _P, c_int64, c_int64, c_int, c_int, c_float, _P, _P, _P, _P,
+                                    _P, _P, _P, _P, _P, _P]),
 }
 
 _lock = threading.Lock()

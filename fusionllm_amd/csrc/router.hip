@@ -46,7 +46,8 @@ template <int EB>
 __device__ __forceinline__ void route_token(const float* lg, const uint16_t* __restrict__ bg, int E, int k,
                                             float route_scale, int lane16, bool active, int t,
                                             int32_t* __restrict__ idx, int64_t* __restrict__ idx64,
-                                            float* __restrict__ wout, float* __restrict__ vout) {
+                                            float* __restrict__ wout, float* __restrict__ vout,
+                                            int* idx_lds = nullptr) {
   float s[EB];
 #pragma unroll
   for (int e = 0; e < EB; ++e) s[e] = (e < E) ? fm_sigmoid(lg[e] + bf2f(bg[e])) : 0.0f;
@@ -73,6 +74,7 @@ __device__ __forceinline__ void route_token(const float* lg, const uint16_t* __r
   if (active && lane16 < k) {
     const int64_t o = static_cast<int64_t>(t) * k + lane16;
     idx[o] = e_sel;
+    if (idx_lds) idx_lds[o] = e_sel;
     if (idx64) idx64[o] = e_sel;
     wout[o] = (v_sel / denom) * route_scale;
     vout[o] = v_sel;
@@ -203,6 +205,127 @@ __global__ __launch_bounds__(512) void router_small_kernel(
   }
   __syncthreads();
   if (grp == 0) route_token<EB>(lsh, bg, E, k, route_scale, lane16, true, t, idx, idx64, wout, vout);
+}
+
+// ---- routing and dispatch of a tiny batch in one launch ---------------------
+// T <= kTinyT tokens: one 512-thread workgroup forms all T * E logits (16-lane
+// group g takes the (token, expert) pairs g, g + 32, ..., each summed in the
+// order described at the top), routes every token (route_token, group t for
+// token t), then does the dispatch of fmoe_dispatch on the T * k slots it
+// holds in LDS: the same stable counting sort (ranks by wave ballots, wave
+// counts added in wave order), the counts and offsets, and the row gather
+// (from the token rows kept in LDS while the logits were formed).  Outputs are
+// those of fmoe_router_fwd followed by fmoe_dispatch, bit for bit.  Meant for
+// T * E <= 64 (one or two logits per 16-lane group); correct for any T <= 16.
+constexpr int kTinyT = 16;
+constexpr int kTinyThreads = 512;  // 256 VGPRs per lane: a token row and a gate row in registers
+constexpr int kTinyWaves = kTinyThreads / 64;
+
+template <int EB, int NQ>
+__global__ __launch_bounds__(kTinyThreads) void route_dispatch_tiny_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, const uint16_t* __restrict__ bg, int T,
+    int dim, int E, int k, float route_scale, int32_t* __restrict__ idx, int64_t* __restrict__ idx64,
+    float* __restrict__ wout, float* __restrict__ vout, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ pos_of_slot,
+    uint4* __restrict__ x_perm) {
+  __shared__ float lsh[kTinyT * EB];
+  __shared__ int idx_sh[kTinyT * FMOE_MAX_TOPK];
+  __shared__ int perm_sh[kTinyT * FMOE_MAX_TOPK];
+  __shared__ int wcount[kTinyWaves][FMOE_MAX_EXPERTS];
+  __shared__ int start[FMOE_MAX_EXPERTS + 1];
+  __shared__ uint4 x_sh[kTinyT * (kRouterMaxDim / 8)];  // the token rows, for the gather
+  const int tid = threadIdx.x, lane16 = tid % kRouterLanes, grp = tid / kRouterLanes;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int nchunk = dim / 8, n_slots = T * k;
+  for (int i = tid; i < kTinyWaves * E; i += kTinyThreads) wcount[i / E][i % E] = 0;
+
+  // 1. logits
+  for (int p = grp; p < T * E; p += kTinyThreads / kRouterLanes) {
+    const int t = p / E, e = p - t * E;
+    const uint4* xrow = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t) * dim);
+    const uint4* wrow = reinterpret_cast<const uint4*>(wg + static_cast<int64_t>(e) * dim);
+    uint4 xr[NQ], wr[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int c = lane16 + kRouterLanes * q;
+      xr[q] = c < nchunk ? xrow[c] : make_uint4(0, 0, 0, 0);
+      wr[q] = c < nchunk ? wrow[c] : make_uint4(0, 0, 0, 0);
+    }
+    if (e == 0) {  // one group per token keeps its row for the gather
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const int c = lane16 + kRouterLanes * q;
+        if (c < nchunk) x_sh[t * nchunk + c] = xr[q];
+      }
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      if (lane16 + kRouterLanes * q < nchunk) {
+        float xf[8], wf[8];
+        unpack8(xr[q], xf);
+        unpack8(wr[q], wf);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc = fmaf(xf[i], wf[i], acc);
+      }
+    }
+#pragma unroll
+    for (int off = kRouterLanes / 2; off >= 1; off >>= 1) acc = acc + xor_lane(acc, off);
+    if (lane16 == 0) lsh[t * EB + e] = acc;
+  }
+  __syncthreads();
+
+  // 2. routing: group t routes token t
+  if (grp < T)
+    route_token<EB>(lsh + grp * EB, bg, E, k, route_scale, lane16, true, grp, idx, idx64, wout, vout, idx_sh);
+  __syncthreads();
+
+  // 3. dispatch: rank slot s among the earlier slots with the same expert
+  const int s = tid;
+  const bool valid = s < n_slots;
+  const int e = valid ? idx_sh[s] : -1;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  uint64_t pending = __ballot(valid);
+  int rank = 0;
+  while (pending) {
+    const int leader = __ffsll(static_cast<unsigned long long>(pending)) - 1;
+    const int le = __shfl(e, leader);
+    const uint64_t m = __ballot(e == le);
+    if (e == le) rank = __popcll(m & lt_mask);
+    if (lane == leader) wcount[wave][le] = __popcll(m);
+    pending &= ~m;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int q = 0; q < E; ++q) {
+      start[q] = run;
+      for (int w = 0; w < kTinyWaves; ++w) run += wcount[w][q];
+    }
+    start[E] = run;
+  }
+  __syncthreads();
+  if (valid) {
+    int pos = start[e] + rank;
+    for (int w = 0; w < wave; ++w) pos += wcount[w][e];
+    perm_sh[pos] = s;
+    perm[pos] = s;
+    pos_of_slot[s] = pos;
+  }
+  for (int q = tid; q < E; q += kTinyThreads) {
+    counts[q] = start[q + 1] - start[q];
+    offsets[q] = start[q];
+  }
+  if (tid == 0) offsets[E] = start[E];
+  if (x_perm == nullptr) return;
+  __syncthreads();
+
+  // 4. row gather from the rows kept in LDS, 16-byte stores
+  const int total = n_slots * nchunk;
+  for (int g = tid; g < total; g += kTinyThreads) {
+    const int r = g / nchunk, c = g - r * nchunk;
+    x_perm[g] = x_sh[(perm_sh[r] / k) * nchunk + c];
+  }
 }
 
 // ---- backward ----------------------------------------------------------------
@@ -382,6 +505,43 @@ extern "C" int fmoe_router_fwd(const void* x, const void* gate_w, const void* ga
   else FMOE_ROUTER_LAUNCH_E(16);
 #undef FMOE_ROUTER_LAUNCH_E
 #undef FMOE_ROUTER_LAUNCH
+  return launch_status();
+}
+
+extern "C" int fmoe_route_dispatch(const void* x, const void* gate_w, const void* gate_b, int64_t T,
+                                   int64_t dim, int n_experts, int k, float route_scale, int32_t* idx,
+                                   int64_t* idx64, float* weights, float* topv, int32_t* counts,
+                                   int32_t* offsets, int32_t* perm, int32_t* pos_of_slot, void* x_perm,
+                                   void* stream) {
+  if (T < 0 || dim <= 0) return FMOE_ERR_INVALID_ARG;
+  if (n_experts <= 0 || n_experts > FMOE_MAX_EXPERTS) return FMOE_ERR_TOO_MANY_EXPERTS;
+  if (k <= 0 || k > FMOE_MAX_TOPK || k > n_experts || dim % 64 != 0 || dim > kRouterMaxDim || T > kTinyT)
+    return FMOE_ERR_SHAPE;
+  if (!counts || !offsets) return FMOE_ERR_INVALID_ARG;
+  if (T > 0 && (!x || !gate_w || !gate_b || !idx || !weights || !topv || !perm || !pos_of_slot))
+    return FMOE_ERR_INVALID_ARG;
+  if (!aligned16(x) || !aligned16(gate_w) || (x_perm && !aligned16(x_perm))) return FMOE_ERR_ALIGN;
+  hipStream_t s = as_stream(stream);
+  auto xs = static_cast<const uint16_t*>(x);
+  auto ws = static_cast<const uint16_t*>(gate_w);
+  auto bs = static_cast<const uint16_t*>(gate_b);
+  auto xp = static_cast<uint4*>(x_perm);
+#define FMOE_TINY(EB, NQ)                                                                                 \
+  route_dispatch_tiny_kernel<EB, NQ><<<1, kTinyThreads, 0, s>>>(xs, ws, bs, (int)T, (int)dim, n_experts, k, \
+                                                                route_scale, idx, idx64, weights, topv,     \
+                                                                counts, offsets, perm, pos_of_slot, xp)
+#define FMOE_TINY_E(NQ)                                  \
+  do {                                                   \
+    if (n_experts <= 8) FMOE_TINY(8, NQ);                \
+    else if (n_experts <= 16) FMOE_TINY(16, NQ);         \
+    else if (n_experts <= 32) FMOE_TINY(32, NQ);         \
+    else FMOE_TINY(64, NQ);                              \
+  } while (0)
+  if (dim <= 512) FMOE_TINY_E(4);
+  else if (dim <= 1024) FMOE_TINY_E(8);
+  else FMOE_TINY_E(16);
+#undef FMOE_TINY_E
+#undef FMOE_TINY
   return launch_status();
 }
 

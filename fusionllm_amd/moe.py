@@ -195,8 +195,12 @@ def _forward_pass(meta, x, gate_w, gate_b, weights, residual=None):
     G = E + (1 if has_shared else 0)
     w1s, w3s, w2s = wb[0::3][:G], wb[1::3][:G], wb[2::3][:G]
 
-    idx, idx64, w, v = K.router_fwd(xb, gwb, gbb, k, rs)
-    counts, offsets, perm, pos, x_perm = K.dispatch(idx, xb, E)
+    if 0 < T <= K.TINY_BATCH and T * E <= 64 and d <= 2048:
+        # decode-sized: routing and dispatch in one launch (one workgroup)
+        idx, idx64, w, v, counts, offsets, perm, pos, x_perm = K.route_dispatch(xb, gwb, gbb, k, rs)
+    else:
+        idx, idx64, w, v = K.router_fwd(xb, gwb, gbb, k, rs)
+        counts, offsets, perm, pos, x_perm = K.dispatch(idx, xb, E)
     rows_r, rows_s = T * k, (T if has_shared else 0)
     ab, h = K.gateup_fwd(x_perm, xb if has_shared else None, offsets, E, w1s, w3s, inter)
     o = K.down_fwd(h, offsets, E, rows_r, rows_s, w2s, d)

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define FMOE_ABI_VERSION 6
+#define FMOE_ABI_VERSION 7
 #define FMOE_MAX_EXPERTS 64
 #define FMOE_MAX_TOPK 8
 #define FMOE_MAX_CAST 64
@@ -101,6 +101,17 @@ int fmoe_dispatch(const int32_t* idx, const void* x, int64_t T, int64_t dim,
                   int32_t* counts, int32_t* offsets, int32_t* perm,
                   int32_t* pos_of_slot, void* x_perm,
                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* Routing and dispatch of a tiny batch (T <= 16 tokens, decode) in one
+ * launch: the outputs of fmoe_router_fwd followed by fmoe_dispatch on its idx,
+ * bit for bit, without the round trip between two launches (moe.py:44-64 for
+ * one decode step).  No workspace.  T > 16 returns FMOE_ERR_SHAPE (use the two
+ * entry points); x_perm may be NULL (no gather). */
+int fmoe_route_dispatch(const void* x, const void* gate_w, const void* gate_b,
+                        int64_t T, int64_t dim, int n_experts, int k, float route_scale,
+                        int32_t* idx, int64_t* idx64, float* weights, float* topv,
+                        int32_t* counts, int32_t* offsets, int32_t* perm,
+                        int32_t* pos_of_slot, void* x_perm, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Grouped gate/up projection with the SwiGLU product fused in the epilogue.

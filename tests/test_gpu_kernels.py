@@ -246,3 +246,22 @@ def test_cast_bf16_bit_exact(gpu_device):
         nan = torch.isnan(want)
         assert torch.equal(torch.isnan(got), nan)
         assert torch.equal(got[~nan].view(torch.int16), want[~nan].view(torch.int16))
+
+
+@pytest.mark.parametrize("T,d,E,k,rs", [(1, 768, 8, 2, 1.0), (8, 768, 8, 2, 1.0), (16, 2048, 64, 6, 2.5),
+                                        (3, 64, 3, 3, 1.0), (5, 256, 33, 8, 1.0), (16, 768, 8, 1, 1.0)])
+def test_route_dispatch_matches_two_launches(gpu_device, T, d, E, k, rs):
+    # The one-launch tiny-batch path gives the outputs of fmoe_router_fwd
+    # followed by fmoe_dispatch, bit for bit (and so the C oracle's).
+    x, gw, gb = _routing_inputs(T, d, E, seed=T * 31 + E)
+    xd, gwd, gbd = x.to(gpu_device), gw.to(gpu_device), gb.to(gpu_device)
+    one = K.route_dispatch(xd, gwd, gbd, k, rs)
+    idx, idx64, w, v = K.router_fwd(xd, gwd, gbd, k, rs)
+    two = (idx, idx64, w, v) + K.dispatch(idx, xd, E)
+    for a, b in zip(one, two):
+        assert torch.equal(a.cpu().view(torch.int32) if a.dtype == torch.float32 else a.cpu(),
+                           b.cpu().view(torch.int32) if b.dtype == torch.float32 else b.cpu())
+    ridx, rw, rv = mo.router_c(x, gw, gb, k, rs)
+    assert torch.equal(one[0].cpu(), ridx)
+    rc, ro, rp, rpos = mo.dispatch_c(one[0].cpu(), E)
+    assert torch.equal(one[4].cpu(), rc) and torch.equal(one[6].cpu(), rp)

@@ -21,7 +21,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     syms = declared_symbols()
-    assert len(syms) == 23
+    assert len(syms) == 24
     for s in syms:
         assert hasattr(lib, s), s
     assert set(syms) == set(_lib.SIGNATURES), "ctypes binding and header disagree"
@@ -71,6 +71,11 @@ def test_argument_errors_without_gpu():
     assert lib.fmoe_cast_bf16(None, None, None, 0, None) == 0
     assert lib.fmoe_cast_bf16(_lib.ptr_array([fake + 4]), _lib.ptr_array([fake]), (ctypes.c_int64 * 1)(8), 1,
                               None) == 3
+    # tiny-batch routing + dispatch: more than 16 tokens is the two-launch path
+    assert lib.fmoe_route_dispatch(None, None, None, 17, 768, 8, 2, 1.0, None, None, None, None, None, None,
+                                   None, None, None, None) == 2
+    assert lib.fmoe_route_dispatch(None, None, None, 4, 768, 8, 2, 1.0, None, None, None, None, None, None,
+                                   None, None, None, None) == 1
     # size queries
     assert lib.fmoe_dispatch_workspace_bytes(16384, 8, 2) == 2 * 128 * 8 * 4
     assert lib.fmoe_weight_grad_workspace_bytes(32768, 16384, 8, 768, 2048) > 0
