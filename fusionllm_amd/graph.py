@@ -1,8 +1,8 @@
 """HIP-graph replay of the DeepSeekMoE forward for decode-sized batches.
 
 At a few tokens per call (workload C3, M = 1 .. 128) the forward is bound by
-host time: five entry points, their argument checks and output allocations
-take longer than the kernels.  ``DecodeGraph`` captures one forward of a
+host time: its four or five entry points, their argument checks and output
+allocations take longer than the kernels.  ``DecodeGraph`` captures one forward of a
 fixed input shape into a HIP graph (torch.cuda.CUDAGraph, which is a HIP
 graph on ROCm) and replays it: the caller writes the tokens into the
 captured input buffer (``__call__`` copies them) and reads the captured
@@ -13,6 +13,9 @@ updated by every replay.  No captured kernel uses hipMemsetAsync.
 
 Inference only (no autograd); the module's parameters must not be
 reallocated after capture (in-place updates are seen by later replays).
+Capture and replay run under the autocast state active at construction
+(an fp32 module needs bf16 autocast around the constructor, as around its
+forward).
 """
 from __future__ import annotations
 
