@@ -262,3 +262,37 @@ def test_bias_update_and_aux_loss_on_gpu(gpu_device, cfg, tokens, train):
     want_bias = mo.gate_bias_step(m.gate.bias, idx, E, 0.001)
     m.update_gate_bias(0.001)
     assert torch.equal(m.gate.bias.detach(), want_bias)
+
+
+@pytest.mark.parametrize("T,dim,inter,E,k,shared,rs", [
+    (1, 64, 64, 1, 1, 0, 1.0),        # one expert, one token
+    (5, 128, 192, 4, 4, 1, 2.5),      # every expert chosen (k = E)
+    (300, 256, 320, 16, 3, 0, 1.0),   # no shared expert, odd inter / 64
+    (7, 768, 2048, 8, 2, 1, 1.0),     # a decode-sized training step (one-launch routing and dispatch)
+    (33, 2048, 1408, 64, 6, 1, 1.0),  # C5 shapes, few tokens
+], ids=["E1", "k_eq_E", "no_shared", "tiny_train", "c5_small"])
+def test_block_edge_shapes(gpu_device, T, dim, inter, E, k, shared, rs):
+    cfg = configs.BlockConfig("edge", T, dim=dim, inter=inter, n_experts=E, topk=k, n_shared=shared,
+                              route_scale=rs, bias="uniform:0.1")
+    data = configs.make_block(cfg, seed=T + E)
+    g = _gpu_run(cfg, data, gpu_device)
+    _routing_exact(data, g, cfg)
+    _compare(cfg, data, g, _oracle_run(cfg, data, g["idx"]))
+
+
+def test_zero_tokens_forward_backward(gpu_device):
+    # An empty batch (the reference's ops on empty tensors): empty output,
+    # zero gradients for the gate and the shared expert, None for the experts.
+    cfg = configs.BlockConfig("empty", 4, dim=128, inter=128, n_experts=4, topk=2)
+    m = build_module(cfg, configs.make_block(cfg, seed=1), gpu_device)
+    x = torch.zeros(2, 0, 128, device=gpu_device, dtype=torch.bfloat16, requires_grad=True)
+    y = m(x)
+    assert y.shape == (2, 0, 128) and m._last_indices.shape == (0, 2)
+    y.sum().backward()
+    assert x.grad.shape == x.shape
+    assert not m.gate.weight.grad.any() and not m.gate.bias.grad.any()
+    assert not m.shared_expert.w1.weight.grad.any()
+    assert all(e.w1.weight.grad is None for e in m.experts)
+    # the reference's formula divides by T*k and averages over no tokens: NaN
+    ref = mo.load_balance_loss(torch.empty(0, 2, dtype=torch.int64), torch.empty(0, 2), 4)
+    assert torch.isnan(ref) and torch.isnan(m.get_load_balance_loss().cpu())
