@@ -394,16 +394,17 @@ class DeepSeekMoE(nn.Module):
         return ws
 
     def _output_dtype(self, x: torch.Tensor, weights: list[torch.Tensor]) -> torch.dtype:
-        params_bf16 = (self.gate.weight.dtype == torch.bfloat16 and self.gate.bias.dtype == torch.bfloat16
-                       and all(w.dtype == torch.bfloat16 for w in weights))
         if torch.is_autocast_enabled("cuda"):
             if torch.get_autocast_dtype("cuda") != torch.bfloat16:
                 raise NotImplementedError("fusionllm_amd.DeepSeekMoE supports bf16 autocast only")
             if x.dtype not in (torch.bfloat16, torch.float32):
                 raise NotImplementedError(f"unsupported input dtype {x.dtype}")
             return x.dtype  # promote(x.dtype, bf16 shared output) for fp32 / bf16 x
-        if x.dtype == torch.bfloat16 and params_bf16:
-            return torch.bfloat16
+        gate = self._modules["gate"]._parameters
+        bf = torch.bfloat16
+        if (x.dtype == bf and gate["weight"].dtype == bf and gate["bias"].dtype == bf
+                and all(w.dtype == bf for w in weights)):
+            return bf
         raise NotImplementedError(
             "fusionllm_amd.DeepSeekMoE computes in bf16: use a bf16 module with bf16 input, or run "
             "under torch.autocast('cuda', dtype=torch.bfloat16)")
@@ -458,30 +459,33 @@ class DeepSeekMoE(nn.Module):
             self._last_indices, self._last_weights = idx64, w
             self._last_counts, self._counts_of = counts, idx64
             return y
-        meta = (E, k, self.moe_inter_dim, float(self.route_scale), self.shared_expert is not None, out_dtype)
+        # Direct dict access to the submodules and parameters: nn.Module's
+        # __getattr__ / __setattr__ cost host time a decode-sized call notices.
+        mods = self._modules
+        gate = mods["gate"]._parameters
+        gw, gb = gate["weight"], gate["bias"]
+        has_shared = mods.get("shared_expert") is not None  # None is a plain attribute, not in _modules
+        meta = (E, k, self.moe_inter_dim, float(self.route_scale), has_shared, out_dtype)
         needs_grad = torch.is_grad_enabled() and (
-            flat.requires_grad or self.gate.weight.requires_grad or self.gate.bias.requires_grad
+            flat.requires_grad or gw.requires_grad or gb.requires_grad
             or any(t.requires_grad for t in weights) or (norm_w is not None and norm_w.requires_grad))
         # Switch devices only when needed (the context manager costs host time).
         switch = flat.device.index != torch._C._cuda_getDevice()
         with torch.cuda.device(flat.device) if switch else contextlib.nullcontext():
             if needs_grad and fused_norm:
-                y, idx64, w, counts = _NormMoEResidualFunction.apply(
-                    meta, eps, flat, norm_w, self.gate.weight, self.gate.bias, *weights)
+                y, idx64, w, counts = _NormMoEResidualFunction.apply(meta, eps, flat, norm_w, gw, gb, *weights)
             elif needs_grad:
-                y, idx64, w, counts = _MoEBlockFunction.apply(meta, flat, self.gate.weight, self.gate.bias,
-                                                              *weights)
+                y, idx64, w, counts = _MoEBlockFunction.apply(meta, flat, gw, gb, *weights)
             else:
                 # inference: the same kernels, nothing kept for a backward pass
                 x_in, residual = flat, None
                 if fused_norm:
                     residual = flat.contiguous()
                     x_in, _ = K.rmsnorm_fwd(residual, None if norm_w is None else norm_w.contiguous(), eps)
-                fw = _forward_pass(meta, x_in, self.gate.weight, self.gate.bias, weights, residual)
+                fw = _forward_pass(meta, x_in, gw, gb, weights, residual)
                 idx64, w, counts, y = fw[4], fw[5], fw[7], fw[-1]
-        self._last_indices = idx64
-        self._last_weights = w
-        self._last_counts, self._counts_of = counts, idx64
+        # plain attributes (not parameters, buffers or submodules)
+        self.__dict__.update(_last_indices=idx64, _last_weights=w, _last_counts=counts, _counts_of=idx64)
         return y
 
     def _forward_empty(self, flat: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
