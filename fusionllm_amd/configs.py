@@ -1,6 +1,7 @@
-"""Workload definitions: the MoE block shapes of BASELINE.json and a seeded
-synthetic generator (random-init weights of the reference architecture;
-there are no checkpoints or datasets).
+"""Workload definitions: the MoE block shapes the benchmark and the parity
+tests use (C1-C5 below) and a seeded synthetic generator (random-init
+weights of the reference architecture; there are no checkpoints or
+datasets).
 
 Shapes follow FusionLLM's benchmark config (training/benchmark.py:10-45:
 dim 768, 8 routed experts, top-2, 1 shared, moe_inter_dim 2048) and the
