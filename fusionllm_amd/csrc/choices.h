@@ -35,6 +35,16 @@ __device__ __forceinline__ void load_sorted_choices(const int32_t* idx, const in
       c.slot[j] = j;
     }
   }
+  // k <= 2 (the reference's top-2 configurations): at most one swap.
+  if (k <= 2) {
+    if (k == 2 && c.e[0] > c.e[1]) {
+      int te = c.e[0]; c.e[0] = c.e[1]; c.e[1] = te;
+      int tp = c.pos[0]; c.pos[0] = c.pos[1]; c.pos[1] = tp;
+      float tw = c.w[0]; c.w[0] = c.w[1]; c.w[1] = tw;
+      int ts = c.slot[0]; c.slot[0] = c.slot[1]; c.slot[1] = ts;
+    }
+    return;
+  }
   // Odd-even transposition sort on 8 entries (padding sorts to the end).
 #pragma unroll
   for (int pass = 0; pass < FMOE_MAX_TOPK; ++pass) {
