@@ -26,7 +26,8 @@
 // partials that wgrad_reduce_kernel adds in chunk order.
 //
 // Decode-sized launches send groups of at most kSmallM rows to
-// small_gemm_kernel, which streams the weights once.
+// small_gemm_kernel, which streams the weights once (when no group of the
+// launch can exceed 2 kSmallM rows, every group, in slabs of kSmallM).
 #include <atomic>
 
 #include "fmoe_common.h"
@@ -587,9 +588,9 @@ __global__ __launch_bounds__(small_waves<MODE>() * 64) void small_gemm_kernel(co
     }
     if (M == 0 || M > args.small_max) return;
   }
-  const uint16_t* A = (g < args.E || args.a_shared == nullptr)
-                          ? args.a_routed + static_cast<int64_t>(row_base) * args.lda
-                          : args.a_shared;
+  const uint16_t* A_group = (g < args.E || args.a_shared == nullptr)
+                                ? args.a_routed + static_cast<int64_t>(row_base) * args.lda
+                                : args.a_shared;
   // Fragments (operands swapped: srcA = weight rows, srcB = activation rows):
   // lane l supplies row l % 16 of each, K elements 8 (l / 16) .. +7 of a step,
   // and gets C[m = l % 16][n = 4 (l / 16) + 0..3].
@@ -597,93 +598,100 @@ __global__ __launch_bounds__(small_waves<MODE>() * 64) void small_gemm_kernel(co
   const uint16_t* w0 = args.b0[g] + static_cast<int64_t>(cb * 16 + r16) * args.ldb + kq;
   const uint16_t* w1 = (MODE == GATEUP_FWD) ? args.b1[g] + static_cast<int64_t>(cb * 16 + r16) * args.ldb + kq
                                             : nullptr;
-  const int mb_n = (M + 15) / 16;  // 1 .. MB
-  const uint16_t* ap[MB];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-    ap[mb] = A + static_cast<int64_t>(min(16 * mb + r16, M - 1)) * args.lda + kq;
   const int nsteps = args.K / 32;
   const int s_begin = wave * nsteps / kSmallWaves, s_end = (wave + 1) * nsteps / kSmallWaves;
+  // A group of more than kSmallM rows (at most small_max = 2 kSmallM) runs as
+  // slabs of kSmallM rows, each streaming the weights again.
+  const int M_group = M, row_base_group = row_base;
+  for (int slab = 0; slab < M_group; slab += kSmallM) {
+    const int M = min(kSmallM, M_group - slab), row_base = row_base_group + slab;
+    const uint16_t* A = A_group + static_cast<int64_t>(slab) * args.lda;
+    const int mb_n = (M + 15) / 16;  // 1 .. MB
+    const uint16_t* ap[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+      ap[mb] = A + static_cast<int64_t>(min(16 * mb + r16, M - 1)) * args.lda + kq;
 
-  f32x4 acc[MB][NB];
+    f32x4 acc[MB][NB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-    for (int b = 0; b < NB; ++b) acc[mb][b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-  for (int s0 = s_begin; s0 < s_end; s0 += CH) {
-    bf16x8 bw[CH][NB], af[CH][MB];
+      for (int b = 0; b < NB; ++b) acc[mb][b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = s_begin; s0 < s_end; s0 += CH) {
+      bf16x8 bw[CH][NB], af[CH][MB];
 #pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      if (s0 + u < s_end) {
-        const int k = 32 * (s0 + u);
-        bw[u][0] = *reinterpret_cast<const bf16x8*>(w0 + k);
-        if constexpr (NB == 2) bw[u][1] = *reinterpret_cast<const bf16x8*>(w1 + k);
+      for (int u = 0; u < CH; ++u) {
+        if (s0 + u < s_end) {
+          const int k = 32 * (s0 + u);
+          bw[u][0] = *reinterpret_cast<const bf16x8*>(w0 + k);
+          if constexpr (NB == 2) bw[u][1] = *reinterpret_cast<const bf16x8*>(w1 + k);
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-          if (mb < mb_n) af[u][mb] = *reinterpret_cast<const bf16x8*>(ap[mb] + k);
+          for (int mb = 0; mb < MB; ++mb)
+            if (mb < mb_n) af[u][mb] = *reinterpret_cast<const bf16x8*>(ap[mb] + k);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        if (s0 + u < s_end) {
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+            if (mb < mb_n)
+#pragma unroll
+              for (int b = 0; b < NB; ++b)
+                acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw[u][b], af[u][mb], acc[mb][b], 0, 0, 0);
+        }
       }
     }
+    // Passes of PASS m blocks: every wave parks its partials, wave p of the pass
+    // adds the eight partials of m block (pass base + p) in wave order and stores.
+    const int m = lane & 15, n0 = cb * 16 + (lane >> 4) * 4;
+    for (int base = 0; base < mb_n; base += PASS) {
 #pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      if (s0 + u < s_end) {
+      for (int p = 0; p < PASS; ++p) {
+        const int mb = base + p;
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-          if (mb < mb_n)
+        for (int q = 0; q < MB; ++q)  // static register index
+          if (q == mb)
 #pragma unroll
             for (int b = 0; b < NB; ++b)
-              acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw[u][b], af[u][mb], acc[mb][b], 0, 0, 0);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) red[wave][p][b][r][lane] = acc[q][b][r];
       }
-    }
-  }
-  // Passes of PASS m blocks: every wave parks its partials, wave p of the pass
-  // adds the eight partials of m block (pass base + p) in wave order and stores.
-  const int m = lane & 15, n0 = cb * 16 + (lane >> 4) * 4;
-  for (int base = 0; base < mb_n; base += PASS) {
+      __syncthreads();
+      const int mb = base + wave;
+      if (wave < PASS && mb < mb_n && 16 * mb + m < M) {
+        float v[NB][4];
 #pragma unroll
-    for (int p = 0; p < PASS; ++p) {
-      const int mb = base + p;
+        for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int q = 0; q < MB; ++q)  // static register index
-        if (q == mb)
+          for (int r = 0; r < 4; ++r) {
+            float t = red[0][wave][b][r][lane];
 #pragma unroll
-          for (int b = 0; b < NB; ++b)
+            for (int w = 1; w < kSmallWaves; ++w) t = t + red[w][wave][b][r][lane];
+            v[b][r] = t;
+          }
+        const int64_t row = row_base + 16 * mb + m;
+        if constexpr (MODE == GATEUP_FWD) {
+          float hv[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) red[wave][p][b][r][lane] = acc[q][b][r];
-    }
-    __syncthreads();
-    const int mb = base + wave;
-    if (wave < PASS && mb < mb_n && 16 * mb + m < M) {
-      float v[NB][4];
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float t = red[0][wave][b][r][lane];
-#pragma unroll
-          for (int w = 1; w < kSmallWaves; ++w) t = t + red[w][wave][b][r][lane];
-          v[b][r] = t;
+          for (int r = 0; r < 4; ++r) {
+            v[0][r] = bf_round(v[0][r]);
+            v[1][r] = bf_round(v[1][r]);
+            hv[r] = bf_round(v[0][r] * fast_sigmoid(v[0][r])) * v[1][r];
+          }
+          uint16_t* ab = args.c0 + row * args.ldc0;
+          *reinterpret_cast<uint2*>(ab + n0) = make_uint2(pack2(v[0][0], v[0][1]), pack2(v[0][2], v[0][3]));
+          *reinterpret_cast<uint2*>(ab + args.inter + n0) =
+              make_uint2(pack2(v[1][0], v[1][1]), pack2(v[1][2], v[1][3]));
+          *reinterpret_cast<uint2*>(args.c1 + row * args.ldc1 + n0) =
+              make_uint2(pack2(hv[0], hv[1]), pack2(hv[2], hv[3]));
+        } else {
+          *reinterpret_cast<uint2*>(args.c0 + row * args.ldc0 + n0) =
+              make_uint2(pack2(v[0][0], v[0][1]), pack2(v[0][2], v[0][3]));
         }
-      const int64_t row = row_base + 16 * mb + m;
-      if constexpr (MODE == GATEUP_FWD) {
-        float hv[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          v[0][r] = bf_round(v[0][r]);
-          v[1][r] = bf_round(v[1][r]);
-          hv[r] = bf_round(v[0][r] * fast_sigmoid(v[0][r])) * v[1][r];
-        }
-        uint16_t* ab = args.c0 + row * args.ldc0;
-        *reinterpret_cast<uint2*>(ab + n0) = make_uint2(pack2(v[0][0], v[0][1]), pack2(v[0][2], v[0][3]));
-        *reinterpret_cast<uint2*>(ab + args.inter + n0) =
-            make_uint2(pack2(v[1][0], v[1][1]), pack2(v[1][2], v[1][3]));
-        *reinterpret_cast<uint2*>(args.c1 + row * args.ldc1 + n0) =
-            make_uint2(pack2(hv[0], hv[1]), pack2(hv[2], hv[3]));
-      } else {
-        *reinterpret_cast<uint2*>(args.c0 + row * args.ldc0 + n0) =
-            make_uint2(pack2(v[0][0], v[0][1]), pack2(v[0][2], v[0][3]));
       }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
@@ -1017,8 +1025,12 @@ int launch_rows(GemmArgs& a, int64_t rows_routed, int64_t rows_shared, int E, vo
   constexpr bool kHasSmall = (MODE == GATEUP_FWD || MODE == DOWN_FWD);
   a.small_max = (kHasSmall && rows_routed + rows_shared <= kSmallLaunchRows) ? kSmallM : 0;
   // A routed group has at most rows_routed rows: when no group can exceed
-  // small_max, the tiled kernel (and its split reduction) has nothing to do.
-  const bool all_small = a.small_max > 0 && rows_routed <= a.small_max && rows_shared <= a.small_max;
+  // 2 kSmallM rows (the small kernel takes a larger group as two slabs), the
+  // tiled kernel (and its split reduction) would have nothing to do.  This
+  // is the case for a decode step of up to 128 tokens at top-2, whose groups
+  // the host cannot bound more tightly.
+  const bool all_small = a.small_max > 0 && rows_routed <= 2 * kSmallM && rows_shared <= kSmallM;
+  if (all_small) a.small_max = 2 * kSmallM;
   // Upper bound of sum over groups of ceil(M_g / BM): floor(rows/BM) + groups.
   const int64_t tiles = (rows_routed / core::BM + E + ceil_div(rows_shared, core::BM)) * tiles_n;
   if (tiles <= 0) return FMOE_OK;

@@ -116,9 +116,11 @@ def _bf(*shape, scale=1.0, g=None):
 @pytest.mark.parametrize("counts,shared,d,I", [
     ([0, 300, 517], 400, 192, 320), ([1, 2, 700], 0, 768, 2048), ([256, 256], 256, 256, 128),
     # decode-sized launches (groups of <= 128 rows go to the small-group kernel,
-    # built for 1, 2, 4 or 8 blocks of 16 rows from a bound on the group sizes)
+    # built for 1, 2, 4 or 8 blocks of 16 rows from a bound on the group sizes;
+    # with at most 256 routed rows, every group, a larger one as 128-row slabs)
     ([0, 1], 1, 256, 128), ([1, 0, 0, 1, 0, 0, 0, 0], 1, 768, 2048), ([1, 5, 16, 17], 32, 768, 2048),
-    ([33, 64, 100, 128, 7], 128, 192, 320), ([129, 3, 0], 2, 256, 512), ([2], 0, 2048, 1408)])
+    ([33, 64, 100, 128, 7], 128, 192, 320), ([129, 3, 0], 2, 256, 512), ([2], 0, 2048, 1408),
+    ([200, 40, 16], 128, 768, 2048), ([0, 256], 0, 192, 320)])
 def test_gateup_and_down_fwd(gpu_device, counts, shared, d, I):
     g = torch.Generator().manual_seed(1)
     E = len(counts)
