@@ -529,21 +529,125 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 // memory: the weights once, the few activation rows from L2).  The partial
 // tiles are added in wave order through LDS.  MB = 16-row blocks the kernel is built for (the
 // host picks it from a bound on the group sizes; with MB > 2 fewer K steps
-// are in flight, the activation fragments take the registers).  Rows past a
-// group's end repeat its last row and are not stored.
+// are in flight, the activation fragments take the registers); a group that
+// needs fewer blocks runs the 2- or 4-block variant, with more K steps in
+// flight.  Rows past a group's end repeat its last row and are not stored.
 constexpr int kSmallM = 128;
 
 template <int MODE>
 constexpr int small_waves() { return MODE == GATEUP_FWD ? 4 : 8; }
 
+template <int MODE>
+constexpr int small_nb() { return MODE == GATEUP_FWD ? 2 : 1; }  // weight matrices
+constexpr int kSmallPass = 2;  // m blocks reduced per LDS pass
+
+// One slab of at most 16 MB rows of one group: the K loop with CH steps of
+// loads in flight, then the wave-order reduction through LDS and the stores.
+// The MFMA chain of every accumulator runs over the wave's K steps in order,
+// whatever MB and CH are, so the result does not depend on them.
+template <int MODE, int MB>
+__device__ __forceinline__ void small_slab(const GemmArgs& args,
+                                           float (*red)[kSmallPass][small_nb<MODE>()][4][64], int wave,
+                                           int lane, int cb, const uint16_t* A, int M, int row_base,
+                                           const uint16_t* w0, const uint16_t* w1, int s_begin, int s_end) {
+  constexpr int kSmallWaves = small_waves<MODE>();
+  constexpr int NB = small_nb<MODE>();
+  constexpr int CH = MB <= 2 ? 8 : (MB == 4 ? 4 : 2);
+  constexpr int PASS = kSmallPass;
+  const int r16 = lane & 15, kq = (lane >> 4) * 8;
+  const int mb_n = (M + 15) / 16;  // 1 .. MB
+  const uint16_t* ap[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+    ap[mb] = A + static_cast<int64_t>(min(16 * mb + r16, M - 1)) * args.lda + kq;
+
+  f32x4 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[mb][b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = s_begin; s0 < s_end; s0 += CH) {
+    bf16x8 bw[CH][NB], af[CH][MB];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      if (s0 + u < s_end) {
+        const int k = 32 * (s0 + u);
+        bw[u][0] = *reinterpret_cast<const bf16x8*>(w0 + k);
+        if constexpr (NB == 2) bw[u][1] = *reinterpret_cast<const bf16x8*>(w1 + k);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          if (mb < mb_n) af[u][mb] = *reinterpret_cast<const bf16x8*>(ap[mb] + k);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      if (s0 + u < s_end) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          if (mb < mb_n)
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+              acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw[u][b], af[u][mb], acc[mb][b], 0, 0, 0);
+      }
+    }
+  }
+  // Passes of PASS m blocks: every wave parks its partials, wave p of the pass
+  // adds the eight partials of m block (pass base + p) in wave order and stores.
+  const int m = lane & 15, n0 = cb * 16 + (lane >> 4) * 4;
+  for (int base = 0; base < mb_n; base += PASS) {
+#pragma unroll
+    for (int p = 0; p < PASS; ++p) {
+      const int mb = base + p;
+#pragma unroll
+      for (int q = 0; q < MB; ++q)  // static register index
+        if (q == mb)
+#pragma unroll
+          for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wave][p][b][r][lane] = acc[q][b][r];
+    }
+    __syncthreads();
+    const int mb = base + wave;
+    if (wave < PASS && mb < mb_n && 16 * mb + m < M) {
+      float v[NB][4];
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float t = red[0][wave][b][r][lane];
+#pragma unroll
+          for (int w = 1; w < kSmallWaves; ++w) t = t + red[w][wave][b][r][lane];
+          v[b][r] = t;
+        }
+      const int64_t row = row_base + 16 * mb + m;
+      if constexpr (MODE == GATEUP_FWD) {
+        float hv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          v[0][r] = bf_round(v[0][r]);
+          v[1][r] = bf_round(v[1][r]);
+          hv[r] = bf_round(v[0][r] * fast_sigmoid(v[0][r])) * v[1][r];
+        }
+        uint16_t* ab = args.c0 + row * args.ldc0;
+        *reinterpret_cast<uint2*>(ab + n0) = make_uint2(pack2(v[0][0], v[0][1]), pack2(v[0][2], v[0][3]));
+        *reinterpret_cast<uint2*>(ab + args.inter + n0) =
+            make_uint2(pack2(v[1][0], v[1][1]), pack2(v[1][2], v[1][3]));
+        *reinterpret_cast<uint2*>(args.c1 + row * args.ldc1 + n0) =
+            make_uint2(pack2(hv[0], hv[1]), pack2(hv[2], hv[3]));
+      } else {
+        *reinterpret_cast<uint2*>(args.c0 + row * args.ldc0 + n0) =
+            make_uint2(pack2(v[0][0], v[0][1]), pack2(v[0][2], v[0][3]));
+      }
+    }
+    __syncthreads();
+  }
+}
+
 template <int MODE, int MB>
 __global__ __launch_bounds__(small_waves<MODE>() * 64) void small_gemm_kernel(const GemmArgs args) {
   static_assert(MODE == GATEUP_FWD || MODE == DOWN_FWD, "forward products only");
   constexpr int kSmallWaves = small_waves<MODE>();
-  constexpr int NB = (MODE == GATEUP_FWD) ? 2 : 1;  // weight matrices (accumulators per m block)
-  constexpr int CH = MB <= 2 ? 8 : (MB == 4 ? 4 : 2);
-  constexpr int PASS = 2;  // m blocks reduced per LDS pass
-  __shared__ float red[kSmallWaves][PASS][NB][4][64];
+  __shared__ float red[kSmallWaves][kSmallPass][small_nb<MODE>()][4][64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ncb = args.N / 16;
@@ -607,91 +711,21 @@ __global__ __launch_bounds__(small_waves<MODE>() * 64) void small_gemm_kernel(co
     const int M = min(kSmallM, M_group - slab), row_base = row_base_group + slab;
     const uint16_t* A = A_group + static_cast<int64_t>(slab) * args.lda;
     const int mb_n = (M + 15) / 16;  // 1 .. MB
-    const uint16_t* ap[MB];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-      ap[mb] = A + static_cast<int64_t>(min(16 * mb + r16, M - 1)) * args.lda + kq;
-
-    f32x4 acc[MB][NB];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int b = 0; b < NB; ++b) acc[mb][b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    for (int s0 = s_begin; s0 < s_end; s0 += CH) {
-      bf16x8 bw[CH][NB], af[CH][MB];
-#pragma unroll
-      for (int u = 0; u < CH; ++u) {
-        if (s0 + u < s_end) {
-          const int k = 32 * (s0 + u);
-          bw[u][0] = *reinterpret_cast<const bf16x8*>(w0 + k);
-          if constexpr (NB == 2) bw[u][1] = *reinterpret_cast<const bf16x8*>(w1 + k);
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb)
-            if (mb < mb_n) af[u][mb] = *reinterpret_cast<const bf16x8*>(ap[mb] + k);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < CH; ++u) {
-        if (s0 + u < s_end) {
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb)
-            if (mb < mb_n)
-#pragma unroll
-              for (int b = 0; b < NB; ++b)
-                acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw[u][b], af[u][mb], acc[mb][b], 0, 0, 0);
-        }
+    // A launch built for MB blocks runs a smaller slab with fewer blocks and
+    // more K steps in flight.
+    if constexpr (MB >= 4) {
+      if (mb_n <= 2) {
+        small_slab<MODE, 2>(args, red, wave, lane, cb, A, M, row_base, w0, w1, s_begin, s_end);
+        continue;
       }
     }
-    // Passes of PASS m blocks: every wave parks its partials, wave p of the pass
-    // adds the eight partials of m block (pass base + p) in wave order and stores.
-    const int m = lane & 15, n0 = cb * 16 + (lane >> 4) * 4;
-    for (int base = 0; base < mb_n; base += PASS) {
-#pragma unroll
-      for (int p = 0; p < PASS; ++p) {
-        const int mb = base + p;
-#pragma unroll
-        for (int q = 0; q < MB; ++q)  // static register index
-          if (q == mb)
-#pragma unroll
-            for (int b = 0; b < NB; ++b)
-#pragma unroll
-              for (int r = 0; r < 4; ++r) red[wave][p][b][r][lane] = acc[q][b][r];
+    if constexpr (MB >= 8) {
+      if (mb_n <= 4) {
+        small_slab<MODE, 4>(args, red, wave, lane, cb, A, M, row_base, w0, w1, s_begin, s_end);
+        continue;
       }
-      __syncthreads();
-      const int mb = base + wave;
-      if (wave < PASS && mb < mb_n && 16 * mb + m < M) {
-        float v[NB][4];
-#pragma unroll
-        for (int b = 0; b < NB; ++b)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float t = red[0][wave][b][r][lane];
-#pragma unroll
-            for (int w = 1; w < kSmallWaves; ++w) t = t + red[w][wave][b][r][lane];
-            v[b][r] = t;
-          }
-        const int64_t row = row_base + 16 * mb + m;
-        if constexpr (MODE == GATEUP_FWD) {
-          float hv[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            v[0][r] = bf_round(v[0][r]);
-            v[1][r] = bf_round(v[1][r]);
-            hv[r] = bf_round(v[0][r] * fast_sigmoid(v[0][r])) * v[1][r];
-          }
-          uint16_t* ab = args.c0 + row * args.ldc0;
-          *reinterpret_cast<uint2*>(ab + n0) = make_uint2(pack2(v[0][0], v[0][1]), pack2(v[0][2], v[0][3]));
-          *reinterpret_cast<uint2*>(ab + args.inter + n0) =
-              make_uint2(pack2(v[1][0], v[1][1]), pack2(v[1][2], v[1][3]));
-          *reinterpret_cast<uint2*>(args.c1 + row * args.ldc1 + n0) =
-              make_uint2(pack2(hv[0], hv[1]), pack2(hv[2], hv[3]));
-        } else {
-          *reinterpret_cast<uint2*>(args.c0 + row * args.ldc0 + n0) =
-              make_uint2(pack2(v[0][0], v[0][1]), pack2(v[0][2], v[0][3]));
-        }
-      }
-      __syncthreads();
     }
+    small_slab<MODE, MB>(args, red, wave, lane, cb, A, M, row_base, w0, w1, s_begin, s_end);
   }
 }
 
