@@ -533,6 +533,10 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 // needs fewer blocks runs the 2- or 4-block variant, with more K steps in
 // flight.  Rows past a group's end repeat its last row and are not stored.
 constexpr int kSmallM = 128;
+// The host knows the shared expert's row count, so the small kernel takes the
+// shared group as slabs of kSharedSlab rows in workgroups of their own (more
+// workgroups, each with more K steps of loads in flight).
+constexpr int kSharedSlab = 64;
 
 template <int MODE>
 constexpr int small_waves() { return MODE == GATEUP_FWD ? 4 : 8; }
@@ -652,7 +656,7 @@ __global__ __launch_bounds__(small_waves<MODE>() * 64) void small_gemm_kernel(co
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ncb = args.N / 16;
   const int cb = blockIdx.x % ncb;
-  int g, row_base, M;
+  int g, row_base, M, shared_off = 0;
   if (MODE == DOWN_FWD && args.small_compact) {
     // Fewer routed rows than experts: workgroup -> (group, column block) over
     // the groups this kernel takes (1 .. small_max rows: routed experts in
@@ -675,26 +679,32 @@ __global__ __launch_bounds__(small_waves<MODE>() * 64) void small_gemm_kernel(co
       row_base = __shfl(lo, g, 64);
       M = __shfl(m_e, g, 64);
     } else {
-      if (rank != nq || args.rows_shared == 0 || args.rows_shared > args.small_max) return;
+      // the shared expert, slab rank - nq
+      shared_off = (rank - nq) * kSharedSlab;
+      if (args.rows_shared > args.small_max || shared_off >= args.rows_shared) return;
       g = args.E;
-      row_base = args.rows_routed;
-      M = args.rows_shared;
+      row_base = args.rows_routed + shared_off;
+      M = min(kSharedSlab, args.rows_shared - shared_off);
     }
   } else {
-    // one workgroup per (group, column block); empty groups return at once
+    // one workgroup per (routed group or shared slab, column block); empty
+    // groups return at once
     g = blockIdx.x / ncb;
     if (g < args.E) {
       row_base = args.offsets[g];
       M = args.offsets[g + 1] - row_base;
+      if (M == 0 || M > args.small_max) return;
     } else {
-      row_base = args.rows_routed;
-      M = args.rows_shared;
+      shared_off = (g - args.E) * kSharedSlab;
+      if (args.rows_shared > args.small_max || shared_off >= args.rows_shared) return;
+      g = args.E;
+      row_base = args.rows_routed + shared_off;
+      M = min(kSharedSlab, args.rows_shared - shared_off);
     }
-    if (M == 0 || M > args.small_max) return;
   }
   const uint16_t* A_group = (g < args.E || args.a_shared == nullptr)
                                 ? args.a_routed + static_cast<int64_t>(row_base) * args.lda
-                                : args.a_shared;
+                                : args.a_shared + static_cast<int64_t>(shared_off) * args.lda;
   // Fragments (operands swapped: srcA = weight rows, srcB = activation rows):
   // lane l supplies row l % 16 of each, K elements 8 (l / 16) .. +7 of a step,
   // and gets C[m = l % 16][n = 4 (l / 16) + 0..3].
@@ -1083,10 +1093,14 @@ int launch_rows(GemmArgs& a, int64_t rows_routed, int64_t rows_shared, int E, vo
       // at most rows_routed routed groups that have rows
       a.small_compact = (MODE == DOWN_FWD && rows_routed < E) ? 1 : 0;
       const int64_t Gr = a.small_compact ? rows_routed : E;
-      const int64_t G = Gr + (rows_shared > 0 ? 1 : 0);
+      const int64_t shared_slabs =
+          (rows_shared > 0 && rows_shared <= a.small_max) ? ceil_div(rows_shared, kSharedSlab) : 0;
+      const int64_t G = Gr + shared_slabs;
+      if (G == 0) return launch_status();
       const dim3 grid(G * (a.N / 16)), block(small_waves<MODE>() * 64);
       hipStream_t s = as_stream(stream);
-      switch (small_blocks(rows_routed > rows_shared ? rows_routed : rows_shared)) {
+      const int64_t shared_bound = rows_shared < kSharedSlab ? rows_shared : kSharedSlab;
+      switch (small_blocks(rows_routed > shared_bound ? rows_routed : shared_bound)) {
         case 1: small_gemm_kernel<MODE, 1><<<grid, block, 0, s>>>(a); break;
         case 2: small_gemm_kernel<MODE, 2><<<grid, block, 0, s>>>(a); break;
         case 4: small_gemm_kernel<MODE, 4><<<grid, block, 0, s>>>(a); break;

@@ -120,7 +120,9 @@ def _bf(*shape, scale=1.0, g=None):
     # with at most 256 routed rows, every group, a larger one as 128-row slabs)
     ([0, 1], 1, 256, 128), ([1, 0, 0, 1, 0, 0, 0, 0], 1, 768, 2048), ([1, 5, 16, 17], 32, 768, 2048),
     ([33, 64, 100, 128, 7], 128, 192, 320), ([129, 3, 0], 2, 256, 512), ([2], 0, 2048, 1408),
-    ([200, 40, 16], 128, 768, 2048), ([0, 256], 0, 192, 320)])
+    ([200, 40, 16], 128, 768, 2048), ([0, 256], 0, 192, 320),
+    # the shared group as 64-row slabs (also with fewer routed rows than experts)
+    ([3, 90], 100, 256, 512), ([1, 0, 0, 0, 0, 0, 0, 0], 100, 256, 512)])
 def test_gateup_and_down_fwd(gpu_device, counts, shared, d, I):
     g = torch.Generator().manual_seed(1)
     E = len(counts)
