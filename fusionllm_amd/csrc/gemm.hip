@@ -529,9 +529,9 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 // memory: the weights once, the few activation rows from L2).  The partial
 // tiles are added in wave order through LDS.  MB = 16-row blocks the kernel is built for (the
 // host picks it from a bound on the group sizes; with MB > 2 fewer K steps
-// are in flight, the activation fragments take the registers); a group that
-// needs fewer blocks runs the 2- or 4-block variant, with more K steps in
-// flight.  Rows past a group's end repeat its last row and are not stored.
+// are in flight, the activation fragments take the registers; a group of
+// more than 16 MB rows runs as slabs of 16 MB rows); a slab that needs fewer
+// blocks runs the 2- or 4-block variant, with more K steps in flight.  Rows past a group's end repeat its last row and are not stored.
 constexpr int kSmallM = 128;
 // The host knows the shared expert's row count, so the small kernel takes the
 // shared group as slabs of kSharedSlab rows in workgroups of their own (more
@@ -651,7 +651,7 @@ __device__ __forceinline__ void small_slab(const GemmArgs& args,
 // SIMD, one more than the compiler picks by itself, without spills: a
 // decode launch of a few thousand waves then needs fewer rounds (C3 M = 32:
 // gate/up 15.8 -> 14.1 us, down 13.0 -> 11.6 us).  The 1-block variant is
-// faster without the bound, the 8-block variants would spill under it.
+// faster without the bound, the 8-block gate/up variant would spill.
 template <int MODE, int MB>
 __global__ __launch_bounds__(small_waves<MODE>() * 64)
 __attribute__((amdgpu_waves_per_eu((MB == 2 || MB == 4) ? (MODE == GATEUP_FWD ? 3 : 4) : 1))) void small_gemm_kernel(
@@ -721,11 +721,11 @@ __attribute__((amdgpu_waves_per_eu((MB == 2 || MB == 4) ? (MODE == GATEUP_FWD ? 
                                             : nullptr;
   const int nsteps = args.K / 32;
   const int s_begin = wave * nsteps / kSmallWaves, s_end = (wave + 1) * nsteps / kSmallWaves;
-  // A group of more than kSmallM rows (at most small_max = 2 kSmallM) runs as
-  // slabs of kSmallM rows, each streaming the weights again.
+  // A group of more than 16 MB rows (at most small_max = 2 kSmallM) runs as
+  // slabs of 16 MB rows, each streaming the weights again.
   const int M_group = M, row_base_group = row_base;
-  for (int slab = 0; slab < M_group; slab += kSmallM) {
-    const int M = min(kSmallM, M_group - slab), row_base = row_base_group + slab;
+  for (int slab = 0; slab < M_group; slab += 16 * MB) {
+    const int M = min(16 * MB, M_group - slab), row_base = row_base_group + slab;
     const uint16_t* A = A_group + static_cast<int64_t>(slab) * args.lda;
     const int mb_n = (M + 15) / 16;  // 1 .. MB
     // A launch built for MB blocks runs a smaller slab with fewer blocks and
@@ -1063,10 +1063,13 @@ int device_cus() {
 }
 
 // 16-row blocks of the small-group kernel for a launch whose groups have at
-// most max_rows rows (a power of two, 1 .. kSmallM / 16).
+// most max_rows rows (1, 2, 4 or 8; the down product stops at 4, so that
+// its larger groups run as 64-row slabs: measured faster, as its 8-block
+// variant holds fewer waves per SIMD).
+template <int MODE>
 inline int small_blocks(int64_t max_rows) {
   const int64_t mb = ceil_div(max_rows < kSmallM ? max_rows : kSmallM, 16);
-  return mb <= 1 ? 1 : mb <= 2 ? 2 : mb <= 4 ? 4 : 8;
+  return mb <= 1 ? 1 : mb <= 2 ? 2 : (mb <= 4 || MODE == DOWN_FWD) ? 4 : 8;
 }
 
 template <int MODE>
@@ -1107,11 +1110,13 @@ int launch_rows(GemmArgs& a, int64_t rows_routed, int64_t rows_shared, int E, vo
       const dim3 grid(G * (a.N / 16)), block(small_waves<MODE>() * 64);
       hipStream_t s = as_stream(stream);
       const int64_t shared_bound = rows_shared < kSharedSlab ? rows_shared : kSharedSlab;
-      switch (small_blocks(rows_routed > shared_bound ? rows_routed : shared_bound)) {
+      switch (small_blocks<MODE>(rows_routed > shared_bound ? rows_routed : shared_bound)) {
         case 1: small_gemm_kernel<MODE, 1><<<grid, block, 0, s>>>(a); break;
         case 2: small_gemm_kernel<MODE, 2><<<grid, block, 0, s>>>(a); break;
         case 4: small_gemm_kernel<MODE, 4><<<grid, block, 0, s>>>(a); break;
-        default: small_gemm_kernel<MODE, 8><<<grid, block, 0, s>>>(a); break;
+        default:
+          if constexpr (MODE != DOWN_FWD) small_gemm_kernel<MODE, 8><<<grid, block, 0, s>>>(a);
+          break;
       }
     }
   }
