@@ -197,11 +197,58 @@ def hbm_traffic(cfg_name, entry):
     return round(sum((k["FETCH_SIZE_KiB"] * fs + k["WRITE_SIZE_KiB"] * ws) * 1024.0 for k in ks))
 
 
+def cpu_info() -> dict:
+    """Host CPU model, logical CPUs and the ISA extensions that set torch's
+    CPU GEMM rate (AVX-512, its bf16 dot products, AMX tiles)."""
+    model, flags = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    want = ("avx2", "fma", "avx512f", "avx512_bf16", "avx512_vnni", "avx512_fp16", "amx_tile", "amx_bf16")
+    return {"cpu_model": model, "nproc": os.cpu_count(), "isa": [f for f in want if f in flags]}
+
+
+def cpu_c1_forward(runs=3):
+    """BASELINE.md's CPU baseline: workload C1, the reference forward
+    (models/moe.py:79-87, module semantics) in fp32 on the host cores at
+    T = 16384 (x [8, 2048, 768] from N(0,1) seed 0, weights N(0, 0.02^2),
+    zero bias); one warmup, then the median of `runs` timed forwards."""
+    from fusionllm_amd import configs
+    from oracle import moe_oracle as mo
+    cfg = configs.C1
+    data = configs.make_block(cfg, seed=0, with_dy=False)
+    sd = data.state_dict()
+    experts = [(sd[f"experts.{e}.w1.weight"], sd[f"experts.{e}.w3.weight"], sd[f"experts.{e}.w2.weight"])
+               for e in range(cfg.n_experts)]
+    shared = (sd["shared_expert.w1.weight"], sd["shared_expert.w3.weight"], sd["shared_expert.w2.weight"])
+    x = data.x.view(*cfg.x_shape)
+    times = []
+    with torch.no_grad():
+        for i in range(runs + 1):
+            t0 = time.perf_counter()
+            mo.moe_forward(x, sd["gate.weight"], sd["gate.bias"], experts, shared, cfg.topk, cfg.route_scale,
+                           mode="module")
+            if i > 0:
+                times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"workload": cfg.name, "tokens": cfg.tokens, "pass": "forward", "dtype": "f32",
+            "value": round(cfg.tokens / med, 1), "unit": "tokens/s", "median_s": round(med, 4),
+            "runs_s": [round(t, 4) for t in times], "cores": torch.get_num_threads(),
+            "gflops": round(cfg.flops_fwd_bwd() / 3 / med / 1e9, 1)}
+
+
 def cpu_baseline(cfg, data, n_tokens, seconds=12.0):
     """Reference algorithm on host cores: the oracle's torch-CPU restatement of
     models/moe.py, bf16, forward + backward, on the first n_tokens tokens,
     repeated until about `seconds` of CPU work (at least 3 passes, at most
-    2.5x that time); value = tokens processed / time of the timed passes."""
+    2.5x that time); value = n_tokens / the median pass time.  Also runs
+    BASELINE.md's C1 fp32 forward (cpu_c1_forward) and names the host CPU."""
     from oracle import moe_oracle as mo
     threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count() or 1
     torch.set_num_threads(threads)
@@ -237,16 +284,19 @@ def cpu_baseline(cfg, data, n_tokens, seconds=12.0):
         t0 = time.perf_counter()
         step()
         times.append(time.perf_counter() - t0)
-    return {
-        "value": T * len(times) / sum(times),
+    out = {
+        "value": round(T / statistics.median(times), 1),
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": (f"{cfg.name}: first {T} of {cfg.tokens} tokens"
                    + (f", {cfg.layers} x (RMSNorm + MoE + residual)" if cfg.layers > 1 else "")
                    + f", reference module semantics (bf16 router), bf16 forward+backward in torch CPU, "
-                   f"{len(times)} passes ({sum(times):.1f} s) after 1 warmup"),
+                   f"median of {len(times)} passes ({sum(times):.1f} s) after 1 warmup"),
     }
+    out.update(cpu_info())
+    out["c1_fp32_forward"] = cpu_c1_forward()
+    return out
 
 
 def optimizer_bench(args):

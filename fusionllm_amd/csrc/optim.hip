@@ -6,10 +6,14 @@
 // fp32; "a + s*b" forms as one fused multiply-add):
 //   m = T(T(m*b1) + (1-b1)*g)                     exp_avg.mul_(b1).add_(g, alpha=1-b1)
 //   v = T(T(v*b2) + (1-b2)*g*g)                   exp_avg_sq.mul_(b2).addcmul_(g, g, value=1-b2)
-//   den = T(T(T(sqrt(v)) / sqrt(bc2)) + eps)      (exp_avg_sq.sqrt() / bias_corr2**0.5).add_(eps)
-//   u = T(T(m / bc1) / den)                       exp_avg / bias_corr1 / denom
+//   den = T(T(T(sqrt(v)) * i2) + eps)             (exp_avg_sq.sqrt() / bias_corr2**0.5).add_(eps)
+//   u = T(T(m * i1) / den)                        exp_avg / bias_corr1 / denom
 // matrices (ndim >= 2), per row of the last dimension:
-//   r = T(T(T(||u||_2) / (sqrt(C) + eps)) + eps), u = T(u / r)
+//   r = T(T(T(||u||_2) * ir) + eps), u = T(u / r)  row_norm / (C**0.5 + eps); update / (row_rms + eps)
+// A tensor divided by a Python number runs on the GPU as a multiplication by
+// the fp32 reciprocal formed on the host (torch's div_true kernel for a CPU
+// scalar divisor: inv = 1.0f / float(b)); i1, i2 and ir are those
+// reciprocals.  Tensor-by-tensor divisions stay true divisions.
 // weight decay (wd > 0): cautious and matrix: p = T(p * T(1 - T(lr*wd*[T(g*p) > 0])))
 //                         otherwise:          p = T(p * (1 - lr*wd))
 //   p = T(p - lr*u)                               p.add_(update, alpha=-lr)
@@ -32,13 +36,13 @@ struct NormuonArgs {
   int row_start[kOptMaxTensors + 1];  // prefix sums of the row counts
   int cols[kOptMaxTensors];
   int matrix[kOptMaxTensors];         // ndim >= 2: row norm and cautious decay
-  float rms_div[kOptMaxTensors];      // sqrt(cols) + eps, formed in double on the host
+  float inv_rms[kOptMaxTensors];      // 1.0f / float(sqrt(cols) + eps), sqrt(cols) + eps in double
   int n;
   int dtype;
   // The reference's Python scalars as its tensor operations see them: each
   // formed in double on the host, then converted to fp32.
   float b1, om1, b2, om2;      // beta1, 1 - beta1, beta2, 1 - beta2
-  float eps, bc1, bc2s;        // eps, bias_corr1, sqrt(bias_corr2)
+  float eps, inv_bc1, inv_bc2s;  // eps, 1.0f / float(bias_corr1), 1.0f / float(sqrt(bias_corr2))
   float neg_lr, lrwd, decay;   // -lr, lr * wd, 1 - lr * wd
   int decay_on, cautious;      // wd > 0; cautious_wd
 };
@@ -97,8 +101,8 @@ __global__ __launch_bounds__(256) void normuon_kernel(const NormuonArgs a) {
         const float g = gg[i][j];
         m[j] = rnd<DT>(fmaf(a.om1, g, rnd<DT>(m[j] * a.b1)));
         v[j] = rnd<DT>(fmaf(a.om2 * g, g, rnd<DT>(v[j] * a.b2)));
-        const float den = rnd<DT>(rnd<DT>(rnd<DT>(sqrtf(v[j])) / a.bc2s) + a.eps);
-        u[i][j] = rnd<DT>(rnd<DT>(m[j] / a.bc1) / den);
+        const float den = rnd<DT>(rnd<DT>(rnd<DT>(sqrtf(v[j])) * a.inv_bc2s) + a.eps);
+        u[i][j] = rnd<DT>(rnd<DT>(m[j] * a.inv_bc1) / den);
         ss = fmaf(u[i][j], u[i][j], ss);
       }
       st4<DT>(a.m[t], e, m);
@@ -111,7 +115,7 @@ __global__ __launch_bounds__(256) void normuon_kernel(const NormuonArgs a) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) ss = ss + __shfl_xor(ss, off, 64);
     const float nrm = rnd<DT>(sqrtf(ss));
-    rd = rnd<DT>(rnd<DT>(nrm / a.rms_div[t]) + a.eps);
+    rd = rnd<DT>(rnd<DT>(nrm * a.inv_rms[t]) + a.eps);
   }
   const bool cautious = a.cautious && matrix;
   const float lrwd_t = rnd<DT>(a.lrwd);
@@ -168,7 +172,7 @@ extern "C" int fmoe_normuon_step(void* const* params, const void* const* grads, 
     a.row_start[i] = static_cast<int>(total);
     a.cols[i] = static_cast<int>(cols[i]);
     a.matrix[i] = is_matrix[i] != 0;
-    a.rms_div[i] = static_cast<float>(std::sqrt(static_cast<double>(cols[i])) + eps);
+    a.inv_rms[i] = 1.0f / static_cast<float>(std::sqrt(static_cast<double>(cols[i])) + eps);
     total += rows[i];
     if (total > INT32_MAX / 2) return FMOE_ERR_SHAPE;
     max_cols = cols[i] > max_cols ? static_cast<int>(cols[i]) : max_cols;
@@ -181,8 +185,8 @@ extern "C" int fmoe_normuon_step(void* const* params, const void* const* grads, 
   a.b2 = static_cast<float>(beta2);
   a.om2 = static_cast<float>(1.0 - beta2);
   a.eps = static_cast<float>(eps);
-  a.bc1 = static_cast<float>(bias_corr1);
-  a.bc2s = static_cast<float>(std::sqrt(bias_corr2));
+  a.inv_bc1 = 1.0f / static_cast<float>(bias_corr1);
+  a.inv_bc2s = 1.0f / static_cast<float>(std::sqrt(bias_corr2));
   a.neg_lr = static_cast<float>(-lr);
   a.lrwd = static_cast<float>(lr * weight_decay);
   a.decay = static_cast<float>(1.0 - lr * weight_decay);

@@ -8,14 +8,13 @@ graph on ROCm) and replays it: the caller writes the tokens into the
 captured input buffer (``__call__`` copies them) and reads the captured
 output.  The captured kernels are the same launches as the eager forward, so
 a replay returns the eager result bit for bit; the module's
-``_last_indices`` / ``_last_weights`` / counts are the graph's buffers,
-updated by every replay.  No captured kernel uses hipMemsetAsync.
+``_last_indices`` and counts are the graph's buffers, updated by every
+replay, and ``_last_weights`` is formed from the graph's fp32 weights buffer
+when it is read.  No captured kernel uses hipMemsetAsync.
 
 Inference only (no autograd); the module's parameters must not be
 reallocated after capture (in-place updates are seen by later replays).
-Capture and replay run under the autocast state active at construction
-(an fp32 module needs bf16 autocast around the constructor, as around its
-forward).
+Capture and replay run under the autocast state active at construction.
 """
 from __future__ import annotations
 
@@ -47,7 +46,8 @@ class DecodeGraph:
         with torch.no_grad(), torch.cuda.graph(self.graph):
             self.y = module(self.x)
         self.last_indices = module._last_indices
-        self.last_weights = module._last_weights
+        self.route_weights = module._route_weights  # the graph's fp32 weights buffer
+        self.score_dtype = module._score_dtype
         self.last_counts = module._last_counts
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
@@ -62,6 +62,7 @@ class DecodeGraph:
         copy of ``__call__``)."""
         self.graph.replay()
         m = self.module
-        m._last_indices, m._last_weights = self.last_indices, self.last_weights
-        m._last_counts, m._counts_of = self.last_counts, self.last_indices
+        m.__dict__.update(_last_indices=self.last_indices, _route_weights=self.route_weights,
+                          _score_dtype=self.score_dtype, _lw=None, _last_counts=self.last_counts,
+                          _counts_of=self.last_indices)
         return self.y

@@ -17,13 +17,24 @@ Mirrors FusionLLM ``models/moe.py``:
 raises on CPU tensors (there is no CPU fallback).  Numerics follow the
 reference composition with one deliberate change: the router accumulates the
 gate logits in fp32 from the bf16 operands (instead of rounding logits and
-scores to bf16), breaks exact score ties toward the lowest expert index, and
-returns fp32 routing weights.
+scores to bf16) and breaks exact score ties toward the lowest expert index.
+The combine uses the router's fp32 weights; ``_last_weights`` reports them in
+the dtype the reference's scores have (bf16 under autocast or for a bf16
+module).
 
-Supported dtypes: a bf16 module with bf16 input, or any module under
-``torch.autocast("cuda", dtype=torch.bfloat16)`` (the reference trainer's
-mode, training/trainer.py:158), where inputs and weights are used as bf16 and
-gradients come back in each parameter's own dtype.
+Dtypes (the products always run on bf16 operands with fp32 accumulation):
+  * a bf16 module with bf16 input: bf16 output;
+  * any module under ``torch.autocast("cuda", dtype=torch.bfloat16)`` (the
+    reference trainer's mode, training/trainer.py:158): output in the input's
+    dtype (bf16 or fp32), as the reference's ``y_routed.to(x.dtype) +
+    y_shared`` promotes there;
+  * an fp32 module with fp32 input outside autocast (the trainer's
+    ``dtype: fp32`` mode, trainer.py:31,158, and its evaluation,
+    trainer.py:332 -> validation.py:53): the operands are cast to bf16 in one
+    launch, and the output and every gradient come back in fp32.
+Gradients always come back in each parameter's own dtype.  A module and
+input of different dtypes outside autocast raise, as the reference's
+``nn.Linear`` does.
 """
 from __future__ import annotations
 
@@ -79,11 +90,12 @@ class _DenseSwiGLUFunction(torch.autograd.Function):
     rows (the dense FFN of models/fusionllm.py:17-27 and the SwiGLU of
     models/moe.py:11-21 used on its own, models/mtp.py:28): the gate/up product
     with the SiLU*up epilogue, the down product, and their backward (dX with
-    the SwiGLU backward fused, dW1/dW3/dW2).  Output bf16, as the bf16
-    Linears give; input and weight gradients in their own dtypes."""
+    the SwiGLU backward fused, dW1/dW3/dW2).  Output in out_dtype (bf16 as
+    the bf16 Linears give, fp32 for an fp32 module outside autocast); input
+    and weight gradients in their own dtypes."""
 
     @staticmethod
-    def forward(ctx, x, w1, w3, w2):
+    def forward(ctx, x, w1, w3, w2, out_dtype):
         T, d = x.shape
         inter = w1.shape[0]
         xb, w1b, w3b, w2b = _bf16_operands([x, w1, w3, w2])
@@ -92,12 +104,12 @@ class _DenseSwiGLUFunction(torch.autograd.Function):
         y = K.down_fwd(h, off, 1, T, 0, [w2b], d)
         ctx.save_for_backward(xb, ab, h, w1b, w3b, w2b, off)
         ctx.dtypes = (x.dtype, w1.dtype, w3.dtype, w2.dtype)
-        return y
+        return y if out_dtype == torch.bfloat16 else y.to(out_dtype)
 
     @staticmethod
     def backward(ctx, dy):
         xb, ab, h, w1b, w3b, w2b, off = ctx.saved_tensors
-        return _dense_backward(dy, xb, ab, h, w1b, w3b, w2b, off, ctx.dtypes, ctx.needs_input_grad[0])
+        return (*_dense_backward(dy, xb, ab, h, w1b, w3b, w2b, off, ctx.dtypes, ctx.needs_input_grad[0]), None)
 
 
 def _dense_backward(dy, xb, ab, h, w1b, w3b, w2b, off, dtypes, need_dx):
@@ -124,13 +136,35 @@ def _dense_backward(dy, xb, ab, h, w1b, w3b, w2b, off, dtypes, need_dx):
     return dx, dw1, dw3, dw2
 
 
+def _uniform_dtype(what: str, tensors) -> torch.dtype:
+    """Outside autocast: the one dtype (bf16 or fp32) of the input and every
+    parameter.  Mixed dtypes raise, as the reference's nn.Linear does
+    ("expected mat1 and mat2 to have the same dtype")."""
+    dts = {t.dtype for t in tensors}
+    if len(dts) != 1:
+        names = ", ".join(sorted(str(d) for d in dts))
+        raise RuntimeError(f"{what}: input and parameters must have the same dtype outside autocast (got {names})")
+    dt = dts.pop()
+    if dt not in (torch.bfloat16, torch.float32):
+        raise NotImplementedError(f"{what} supports bf16 and fp32 tensors (got {dt})")
+    return dt
+
+
+def _autocast_check(what: str, x: torch.Tensor) -> None:
+    if torch.get_autocast_dtype("cuda") != torch.bfloat16:
+        raise NotImplementedError(f"{what} supports bf16 autocast only")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise NotImplementedError(f"unsupported input dtype {x.dtype}")
+
+
 def dense_swiglu(x: torch.Tensor, w1: torch.Tensor, w3: torch.Tensor, w2: torch.Tensor) -> torch.Tensor:
     """``w2(silu(w1 x) * w3 x)`` for bias-free nn.Linear weights (w1, w3
     [inter, dim], w2 [dim, inter]) on the kernels; any leading shape of x.
 
-    bf16: a bf16 input with bf16 weights, or any input under
-    ``torch.autocast("cuda", dtype=torch.bfloat16)`` (output bf16, as the
-    reference's Linears give there).  ROCm tensors only.
+    Under ``torch.autocast("cuda", dtype=torch.bfloat16)`` the output is bf16,
+    as the reference's Linears give there.  Outside autocast the input and
+    weights share one dtype: bf16 gives bf16; fp32 runs the same bf16 kernels
+    on bf16 copies and returns fp32 (output and gradients).  ROCm tensors only.
     """
     dim = w1.shape[1]
     shape = x.shape
@@ -138,20 +172,16 @@ def dense_swiglu(x: torch.Tensor, w1: torch.Tensor, w3: torch.Tensor, w2: torch.
     if not flat.is_cuda:
         raise RuntimeError("fusionllm_amd SwiGLU runs on a ROCm device only (got a CPU tensor)")
     if torch.is_autocast_enabled("cuda"):
-        if torch.get_autocast_dtype("cuda") != torch.bfloat16:
-            raise NotImplementedError("fusionllm_amd SwiGLU supports bf16 autocast only")
-        if flat.dtype not in (torch.bfloat16, torch.float32):
-            raise NotImplementedError(f"unsupported input dtype {flat.dtype}")
-    elif not (flat.dtype == torch.bfloat16 and all(w.dtype == torch.bfloat16 for w in (w1, w3, w2))):
-        raise NotImplementedError(
-            "fusionllm_amd SwiGLU computes in bf16: use bf16 weights and input, or run under "
-            "torch.autocast('cuda', dtype=torch.bfloat16)")
+        _autocast_check("fusionllm_amd SwiGLU", flat)
+        out_dtype = torch.bfloat16
+    else:
+        out_dtype = _uniform_dtype("fusionllm_amd SwiGLU", (flat, w1, w3, w2))
     if flat.shape[0] == 0:
-        y = flat.new_zeros(0, dim, dtype=torch.bfloat16)
+        y = flat.new_zeros(0, dim, dtype=out_dtype)
         return (y + (w1.sum() + w3.sum() + w2.sum()).to(y.dtype) * 0 + flat.sum().to(y.dtype) * 0).view(shape)
     switch = flat.device.index != torch._C._cuda_getDevice()
     with torch.cuda.device(flat.device) if switch else contextlib.nullcontext():
-        y = _DenseSwiGLUFunction.apply(flat, w1, w3, w2)
+        y = _DenseSwiGLUFunction.apply(flat, w1, w3, w2, out_dtype)
     return y.view(*shape[:-1], w2.shape[0])
 
 
@@ -175,7 +205,10 @@ class SwiGLUExpert(nn.Module):
         if torch.compiler.is_compiling():
             # traced (torch.compile): the fusionllm::swiglu_fwd operator
             flat = x.reshape(-1, w1.shape[1])
-            return torch.ops.fusionllm.swiglu_fwd(flat, w1, w3, w2)[0].view(*x.shape[:-1], w2.shape[0])
+            y = torch.ops.fusionllm.swiglu_fwd(flat, w1, w3, w2)[0]
+            if not torch.is_autocast_enabled("cuda") and x.dtype == torch.float32:
+                y = y.float()  # fp32 module outside autocast: fp32 output
+            return y.view(*x.shape[:-1], w2.shape[0])
         return dense_swiglu(x, w1, w3, w2)
 
 
@@ -374,11 +407,40 @@ class DeepSeekMoE(nn.Module):
         # As in the reference, n_shared_experts > 0 means one shared expert.
         self.shared_expert = SwiGLUExpert(self.dim, self.moe_inter_dim) if self.n_shared_experts > 0 else None
         self._last_indices: torch.Tensor | None = None
-        self._last_weights: torch.Tensor | None = None
+        # The router's fp32 weights of the last forward (bit-exact with the
+        # C oracle) and the dtype the reference's scores have in the same
+        # call; _last_weights converts on first access.
+        self._route_weights: torch.Tensor | None = None
+        self._score_dtype: torch.dtype | None = None
+        self._last_weights = None
         # Per-expert slot counts of the last routing, from the dispatch
         # kernel's histogram, and the indices tensor they were counted from.
         self._last_counts: torch.Tensor | None = None
         self._counts_of: torch.Tensor | None = None
+
+    @property
+    def _last_weights(self) -> torch.Tensor | None:
+        """Routing weights of the last forward, detached (models/moe.py:84), in
+        the dtype the reference's scores have in that call: bf16 for a bf16
+        module or under bf16 autocast (the gate Linear's output dtype), fp32
+        for an fp32 module outside autocast.  The kernels route in fp32; the
+        rounding to bf16 happens here, on first access, so the forward pays
+        no extra launch."""
+        d = self.__dict__
+        w = d.get("_lw")
+        if w is None:
+            rw = d.get("_route_weights")
+            if rw is None:
+                return None
+            dt = d.get("_score_dtype") or rw.dtype
+            w = rw if rw.dtype == dt else rw.to(dt)
+            d["_lw"] = w
+        return w
+
+    @_last_weights.setter
+    def _last_weights(self, value: torch.Tensor | None) -> None:
+        # an assigned value is taken as it is (the reference's attribute)
+        self.__dict__.update(_lw=value, _route_weights=None, _score_dtype=None)
 
     def _flat_weights(self) -> list[torch.Tensor]:
         # Direct dict access: nn.Module.__getattr__ per weight dominates the
@@ -394,20 +456,19 @@ class DeepSeekMoE(nn.Module):
         return ws
 
     def _output_dtype(self, x: torch.Tensor, weights: list[torch.Tensor]) -> torch.dtype:
+        """dtype of the block's output (models/moe.py:77,87: ``y_routed.to(x.dtype)
+        + y_shared``).  Under bf16 autocast the shared output is bf16, so the
+        sum takes x's dtype; outside autocast the module and x share one
+        dtype (bf16, or fp32: bf16 kernels on bf16 copies, fp32 results)."""
         if torch.is_autocast_enabled("cuda"):
-            if torch.get_autocast_dtype("cuda") != torch.bfloat16:
-                raise NotImplementedError("fusionllm_amd.DeepSeekMoE supports bf16 autocast only")
-            if x.dtype not in (torch.bfloat16, torch.float32):
-                raise NotImplementedError(f"unsupported input dtype {x.dtype}")
-            return x.dtype  # promote(x.dtype, bf16 shared output) for fp32 / bf16 x
-        gate = self._modules["gate"]._parameters
+            _autocast_check("fusionllm_amd.DeepSeekMoE", x)
+            return x.dtype
         bf = torch.bfloat16
-        if (x.dtype == bf and gate["weight"].dtype == bf and gate["bias"].dtype == bf
-                and all(w.dtype == bf for w in weights)):
-            return bf
-        raise NotImplementedError(
-            "fusionllm_amd.DeepSeekMoE computes in bf16: use a bf16 module with bf16 input, or run "
-            "under torch.autocast('cuda', dtype=torch.bfloat16)")
+        gate = self._modules["gate"]._parameters
+        gw, gb = gate["weight"], gate["bias"]
+        if x.dtype == bf and gw.dtype == bf and gb.dtype == bf and all(w.dtype == bf for w in weights):
+            return bf  # the common case, without building a set
+        return _uniform_dtype("fusionllm_amd.DeepSeekMoE", (x, gw, gb, *weights))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         shape = x.shape
@@ -456,7 +517,8 @@ class DeepSeekMoE(nn.Module):
             y, idx64, w, counts = torch.ops.fusionllm.moe_fwd(
                 flat, self.gate.weight, self.gate.bias, weights, k, float(self.route_scale),
                 self.shared_expert is not None, out_dtype)[:4]
-            self._last_indices, self._last_weights = idx64, w
+            score_dtype = torch.bfloat16 if torch.is_autocast_enabled("cuda") else out_dtype
+            self._last_indices, self._last_weights = idx64, w.to(score_dtype)
             self._last_counts, self._counts_of = counts, idx64
             return y
         # Direct dict access to the submodules and parameters: nn.Module's
@@ -485,7 +547,9 @@ class DeepSeekMoE(nn.Module):
                 fw = _forward_pass(meta, x_in, gw, gb, weights, residual)
                 idx64, w, counts, y = fw[4], fw[5], fw[7], fw[-1]
         # plain attributes (not parameters, buffers or submodules)
-        self.__dict__.update(_last_indices=idx64, _last_weights=w, _last_counts=counts, _counts_of=idx64)
+        score_dtype = torch.bfloat16 if torch.is_autocast_enabled("cuda") else out_dtype
+        self.__dict__.update(_last_indices=idx64, _route_weights=w, _score_dtype=score_dtype, _lw=None,
+                             _last_counts=counts, _counts_of=idx64)
         return y
 
     def _forward_empty(self, flat: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
@@ -494,7 +558,8 @@ class DeepSeekMoE(nn.Module):
         # gradients for them, as the reference's empty matmuls do.
         k = self.n_activated_experts
         self._last_indices = torch.empty(0, k, dtype=torch.int64, device=flat.device)
-        self._last_weights = torch.empty(0, k, dtype=torch.float32, device=flat.device)
+        score_dtype = torch.bfloat16 if torch.is_autocast_enabled("cuda") else out_dtype
+        self._last_weights = torch.empty(0, k, dtype=score_dtype, device=flat.device)
         self._last_counts = torch.zeros(self.n_routed_experts, dtype=torch.int32, device=flat.device)
         self._counts_of = self._last_indices
         y = flat.new_zeros(0, self.dim, dtype=out_dtype)

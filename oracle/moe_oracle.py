@@ -161,14 +161,17 @@ def load_balance_loss(indices, weights, n_experts: int):
 
 @torch.no_grad()
 def normuon_step(p, grad, state: dict, lr: float = 0.02, betas=(0.9, 0.95), eps: float = 1e-8,
-                 weight_decay: float = 0.1, cautious_wd: bool = True):
+                 weight_decay: float = 0.1, cautious_wd: bool = True, ops: bool = False):
     """NorMuon.step for one parameter, training/optimizer.py:18-58, op by op;
     updates p and state in place.
 
-    fp32: the reference's tensor operations as written.  bf16: the same
-    operations as torch runs them on the GPU (where the reference trains):
-    fp32 arithmetic with the Python scalars in fp32, each result rounded to
-    bf16, "a + s*b" as one fused multiply-add.  (torch's CPU kernels instead
+    fp32 (and ``ops=True`` for any dtype and device): the reference's tensor
+    operations as written.  bf16: the same operations as torch runs them on
+    the GPU (where the reference trains): fp32 arithmetic with the Python
+    scalars in fp32, each result rounded to bf16, "a + s*b" as one fused
+    multiply-add, and a tensor divided by a Python number as a product with
+    the number's fp32 reciprocal (torch's CUDA div_true kernel does that for a
+    CPU-scalar divisor: inv = 1.0f / float(b)).  (torch's CPU kernels instead
     round the alpha/value scalars of add_/addcmul_ to bf16, which changes
     about a fifth of the first step's exp_avg elements.)
     """
@@ -182,7 +185,7 @@ def normuon_step(p, grad, state: dict, lr: float = 0.02, betas=(0.9, 0.95), eps:
     step_count = state["step"]
     bias_corr1 = 1.0 - beta1 ** step_count
     bias_corr2 = 1.0 - beta2 ** step_count
-    if p.dtype == torch.bfloat16:
+    if p.dtype == torch.bfloat16 and not ops:
         _normuon_bf16(p, grad, exp_avg, exp_avg_sq, lr, beta1, beta2, eps, weight_decay, cautious_wd,
                       bias_corr1, bias_corr2)
         return
@@ -206,16 +209,17 @@ def normuon_step(p, grad, state: dict, lr: float = 0.02, betas=(0.9, 0.95), eps:
 def _normuon_bf16(p, grad, exp_avg, exp_avg_sq, lr, beta1, beta2, eps, weight_decay, cautious_wd,
                   bias_corr1, bias_corr2):
     f32 = lambda v: torch.tensor(v, dtype=torch.float32)  # a Python scalar as the GPU kernels see it
+    inv = lambda v: f32(1.0) / f32(v)  # a Python divisor: its fp32 reciprocal, then a product
     r = lambda t: t.to(torch.bfloat16).float()             # round an operation's result to bf16
     fma = lambda a, b, c: (a.double() * b.double() + c.double()).float()
     g, w = grad.float(), p.float()
     m = r(fma(f32(1.0 - beta1), g, r(exp_avg.float() * f32(beta1))))
     v = r(fma(f32(1.0 - beta2) * g, g, r(exp_avg_sq.float() * f32(beta2))))
-    denom = r(r(r(v.sqrt()) / f32(bias_corr2 ** 0.5)) + f32(eps))
-    update = r(r(m / f32(bias_corr1)) / denom)
+    denom = r(r(r(v.sqrt()) * inv(bias_corr2 ** 0.5)) + f32(eps))
+    update = r(r(m * inv(bias_corr1)) / denom)
     if p.ndim >= 2:
         row_norm = r(update.double().pow(2).sum(-1, keepdim=True).sqrt().float())
-        row_rms = r(row_norm / f32(update.size(-1) ** 0.5 + eps))
+        row_rms = r(row_norm * inv(update.size(-1) ** 0.5 + eps))
         update = r(update / r(row_rms + f32(eps)))
     if weight_decay > 0:
         if cautious_wd and p.ndim >= 2:

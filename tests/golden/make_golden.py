@@ -14,7 +14,10 @@ Fixture layout: one npz, keys "<case>/<name>".  bf16 tensors are stored as
 uint16 bit patterns, fp32 as float32, indices as int64.  Every case records
 its inputs (x, dy, parameters under the reference's state_dict names) and the
 reference's outputs: y, _last_indices, _last_weights, x.grad and each
-parameter's .grad ("none" marker array when the reference leaves it None).
+parameter's .grad ("none" marker array when the reference leaves it None),
+and, from the same module after that forward, the aux outputs:
+get_load_balance_loss() (moe.py:100-109) as "aux/loss" and gate.bias after
+update_gate_bias(AUX_SPEED) (moe.py:89-98) as "aux/bias_after".
 """
 from __future__ import annotations
 
@@ -27,6 +30,7 @@ import torch
 
 HERE = Path(__file__).resolve().parent
 OUT = HERE / "moe_golden.npz"
+AUX_SPEED = 0.01  # update_gate_bias step recorded by every case
 
 # name: (dtype, T, dim, inter, E, k, n_shared, route_scale, bias mode, seed)
 CASES = {
@@ -76,9 +80,13 @@ def make_case(ref, dtype, T, d, I, E, k, n_shared, rs, bias, seed):
     y.backward(dy)
     out = {"x": x, "dy": dy, "y": y, "indices": m._last_indices, "weights": m._last_weights, "dx": x.grad}
     for name, p in m.named_parameters():
-        out[f"param/{name}"] = p
+        out[f"param/{name}"] = p.detach().clone()  # before update_gate_bias below
         out[f"grad/{name}"] = p.grad if p.grad is not None else torch.zeros(0)
         out[f"gradnone/{name}"] = torch.tensor([p.grad is None])
+    # aux outputs from the routing of this forward (models/moe.py:89-109)
+    out["aux/loss"] = m.get_load_balance_loss().detach()
+    m.update_gate_bias(speed=AUX_SPEED)
+    out["aux/bias_after"] = m.gate.bias.detach().clone()
     meta = torch.tensor([T, d, I, E, k, n_shared], dtype=torch.int64)
     out["meta"] = meta
     out["route_scale"] = torch.tensor([rs], dtype=torch.float64)

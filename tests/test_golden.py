@@ -81,3 +81,35 @@ def test_golden_covers_ties_and_empty_experts():
     assert picked != [0, 1], "torch.topk tie order coincides with lowest-index"
     # at least one expert received no tokens, so its gradients are None
     assert any(bool(f[n][0]) for n in f if n.startswith("gradnone/experts."))
+
+
+@pytest.mark.parametrize("case", _cases())
+def test_aux_outputs_reproduce_reference_bitwise(case):
+    # get_load_balance_loss (models/moe.py:100-109) and update_gate_bias
+    # (moe.py:89-98), recorded by the reference module after the case's
+    # forward: the oracle's restatements and the drop-in module's methods
+    # (host torch code on the recorded routing) give the same bits.
+    from fusionllm_amd import DeepSeekMoE
+
+    speed = 0.01  # AUX_SPEED of tests/golden/make_golden.py
+    f = _load(case)
+    dtype = torch.bfloat16 if f["x"].dtype == np.uint16 else torch.float32
+    T, d, I, E, k, n_shared = (int(v) for v in f["meta"])
+    idx = torch.from_numpy(f["indices"].copy())
+    w = _t(f["weights"], dtype)
+    bias = _t(f["param/gate.bias"], dtype)
+    want_loss = f["aux/loss"]
+    want_bias = f["aux/bias_after"].view(np.int16 if dtype == torch.bfloat16 else np.int32)
+
+    assert np.array_equal(_bits(mo.load_balance_loss(idx, w, E).float()), want_loss.view(np.int32))
+    assert np.array_equal(_bits(mo.gate_bias_step(bias, idx, E, speed)), want_bias)
+
+    cfg = {"dim": d, "n_routed_experts": E, "n_shared_experts": n_shared, "n_activated_experts": k,
+           "moe_inter_dim": I, "route_scale": float(f["route_scale"][0])}
+    m = DeepSeekMoE(cfg).to(dtype)
+    with torch.no_grad():
+        m.gate.bias.copy_(bias)
+    m._last_indices, m._last_weights = idx, w
+    assert np.array_equal(_bits(m.get_load_balance_loss().float()), want_loss.view(np.int32))
+    m.update_gate_bias(speed)
+    assert np.array_equal(_bits(m.gate.bias), want_bias)

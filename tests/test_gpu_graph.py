@@ -23,13 +23,14 @@ def test_decode_graph_replays_match_eager(gpu_device, cfg):
     for rep in range(4):
         x = (torch.randn(x0.shape, generator=gen) * (1 + rep)).to(gpu_device, torch.bfloat16)
         y = g(x).clone()
-        idx, w = m._last_indices.clone(), m._last_weights.clone()
+        idx, w, wl = m._last_indices.clone(), m._route_weights.clone(), m._last_weights.clone()
         torch.cuda.synchronize()
         with torch.no_grad():
             want = m(x)  # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int16), want.view(torch.int16)), f"replay {rep}"
-        assert torch.equal(idx, m._last_indices) and torch.equal(w.view(torch.int32), m._last_weights.view(torch.int32))
+        assert torch.equal(idx, m._last_indices) and torch.equal(w.view(torch.int32), m._route_weights.view(torch.int32))
+        assert wl.dtype == torch.bfloat16 and torch.equal(wl.view(torch.int16), m._last_weights.view(torch.int16))
         z = torch.full((1024,), float(rep), device=gpu_device).sum()  # unrelated eager kernels
         assert float(z) == 1024.0 * rep
 

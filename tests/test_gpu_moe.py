@@ -38,7 +38,10 @@ def _gpu_run(cfg, data, dev, backward=True):
     m = build_module(cfg, data, dev)
     x = data.x.to(dev, torch.bfloat16).requires_grad_(backward)
     y = m(x)
-    out = {"y": y.detach().cpu(), "idx": m._last_indices.cpu(), "w": m._last_weights.cpu(), "module": m}
+    # "w": the router's fp32 weights (bit-exact with the C oracle); the
+    # reference-facing _last_weights is their bf16 rounding for a bf16 module
+    assert m._last_weights.dtype == torch.bfloat16
+    out = {"y": y.detach().cpu(), "idx": m._last_indices.cpu(), "w": m._route_weights.cpu(), "module": m}
     if backward:
         y.backward(data.dy.to(dev, torch.bfloat16))
         out["dx"] = x.grad.cpu()

@@ -97,7 +97,7 @@ def _gpu_block(cfg, data, nw, dev, backward=True, dtype=torch.bfloat16):
         norm.weight.copy_(nw)
     x = data.x.to(dev, dtype).requires_grad_(backward)
     out = moe_residual(x, norm, m)
-    res = {"out": out.detach().cpu(), "idx": m._last_indices.cpu(), "w": m._last_weights.cpu(),
+    res = {"out": out.detach().cpu(), "idx": m._last_indices.cpu(), "w": m._route_weights.cpu(),
            "x": x.detach()}
     if backward:
         out.backward(data.dy.to(dev, dtype))

@@ -122,3 +122,31 @@ def test_normuon_on_expert_weights_after_backward(gpu_device):
     for (p0, g0), p in zip(ref, mats):
         mo.normuon_step(p0, g0, {}, lr=0.02, betas=(0.95, 0.95))
         _compare(p, p0, "expert matrix")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_normuon_matches_reference_ops_on_the_gpu(gpu_device, dtype):
+    # The reference's step (training/optimizer.py:35-57) as torch runs it on
+    # the GPU: the oracle's op-by-op restatement (ops=True) on device tensors.
+    # Same tolerances as above; here the bf16 reference is torch's own GPU
+    # kernels (Python-number divisors as fp32 reciprocals, fp32 scalars,
+    # per-operation rounding), not an emulation of them.
+    g = torch.Generator().manual_seed(17)
+    ps = [(torch.randn(*s, generator=g) * 0.02).to(dtype) for s in SHAPES]
+    grads = [[(torch.randn(*s, generator=g) * 1e-3).to(dtype) for s in SHAPES] for _ in range(3)]
+    ref_p = [p.to(gpu_device) for p in ps]
+    ref_st = [{} for _ in ps]
+    dev_p = [torch.nn.Parameter(p.to(gpu_device)) for p in ps]
+    opt = NorMuon(dev_p, lr=0.02, betas=(0.95, 0.95), eps=1e-8, weight_decay=0.1, cautious_wd=True)
+    for step in range(3):
+        for i in range(len(ps)):
+            gd = grads[step][i].to(gpu_device)
+            mo.normuon_step(ref_p[i], gd, ref_st[i], lr=0.02, betas=(0.95, 0.95), eps=1e-8, weight_decay=0.1,
+                            cautious_wd=True, ops=True)
+            dev_p[i].grad = gd
+        opt.step()
+    for i, s in enumerate(SHAPES):
+        st = opt.state[dev_p[i]]
+        _compare(dev_p[i], ref_p[i].cpu(), f"param {s}", update_atol=3 * 0.02 * 2.0 ** -8)
+        _compare(st["exp_avg"], ref_st[i]["exp_avg"].cpu(), f"exp_avg {s}")
+        _compare(st["exp_avg_sq"], ref_st[i]["exp_avg_sq"].cpu(), f"exp_avg_sq {s}")
