@@ -439,8 +439,12 @@ class DeepSeekMoE(nn.Module):
 
     @_last_weights.setter
     def _last_weights(self, value: torch.Tensor | None) -> None:
-        # an assigned value is taken as it is (the reference's attribute)
-        self.__dict__.update(_lw=value, _route_weights=None, _score_dtype=None)
+        # an assigned value is taken as it is (the reference's attribute);
+        # item assignments, which torch.compile traces (dict.update it does not)
+        d = self.__dict__
+        d["_lw"] = value
+        d["_route_weights"] = None
+        d["_score_dtype"] = None
 
     def _flat_weights(self) -> list[torch.Tensor]:
         # Direct dict access: nn.Module.__getattr__ per weight dominates the
