@@ -122,8 +122,9 @@ def route_dispatch(x, gate_w, gate_b, k: int, route_scale: float):
 
 
 @_timed
-def dispatch(idx, x, n_experts: int, gather: bool = True):
-    """Histogram + scan + stable scatter (+ row gather); returns counts, offsets, perm, pos, x_perm."""
+def dispatch(idx, x, n_experts: int, gather: bool = True, noalloc: bool = False):
+    """Histogram + scan + stable scatter (+ row gather); returns counts, offsets, perm, pos, x_perm.
+    noalloc: fmoe_dispatch_noalloc, whose scratch is the library's static device array."""
     lib = _lib.load()
     T, k = idx.shape
     d = x.shape[1]
@@ -133,6 +134,13 @@ def dispatch(idx, x, n_experts: int, gather: bool = True):
     perm = torch.empty(T * k, dtype=torch.int32, device=dev)
     pos = torch.empty(T * k, dtype=torch.int32, device=dev)
     x_perm = torch.empty(T * k, d, dtype=torch.bfloat16, device=dev) if gather else None
+    if noalloc:
+        check(lib.fmoe_dispatch_noalloc(_req(idx, "idx", torch.int32), _req(x, "x", torch.bfloat16), T, d,
+                                        n_experts, k, counts.data_ptr(), offsets.data_ptr(), perm.data_ptr(),
+                                        pos.data_ptr(), x_perm.data_ptr() if x_perm is not None else None,
+                                        _stream()),
+              "fmoe_dispatch_noalloc")
+        return counts, offsets, perm, pos, x_perm
     ws_bytes = lib.fmoe_dispatch_workspace_bytes(T, n_experts, k)
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
     check(lib.fmoe_dispatch(_req(idx, "idx", torch.int32), _req(x, "x", torch.bfloat16), T, d, n_experts, k,

@@ -13,6 +13,10 @@ extern "C" const char* fmoe_status_string(int status) {
     case FMOE_ERR_LAUNCH: return "kernel launch failed";
     case FMOE_ERR_WORKSPACE: return "workspace smaller than the size query returned";
     case FMOE_ERR_TOO_MANY_EXPERTS: return "number of experts outside 1..64";
+    case FMOE_ERR_SCRATCH:
+      return "workload larger than the static scratch of the allocation-free entry point "
+             "(fmoe_dispatch_noalloc: fmoe_dispatch_workspace_bytes(T, E, k) must be <= 1 MiB); "
+             "use fmoe_dispatch with a workspace";
     default: return "unknown status";
   }
 }

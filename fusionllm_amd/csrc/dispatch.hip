@@ -16,6 +16,9 @@
 // exclusive prefix over the waves of the block) and writes perm /
 // pos_of_slot.  Stage 4 copies rows of x into the expert-contiguous buffer
 // with 16-byte loads and stores, many rows per workgroup.
+#include <atomic>
+#include <mutex>
+
 #include "fmoe_common.h"
 
 namespace fmoe {
@@ -253,6 +256,43 @@ extern "C" size_t fmoe_dispatch_workspace_bytes(int64_t T, int n_experts, int k)
   return static_cast<size_t>(2 * nblocks * n_experts) * sizeof(int32_t);
 }
 
+namespace {
+
+// ---- allocation-free variant -----------------------------------------------
+// The scratch of fmoe_dispatch_noalloc (per-block expert counts and bases)
+// lives in this file-scope device array, one copy per GPU for the life of the
+// process.  Host code never passes `scratch` itself to a kernel: on the host
+// it names a stand-in, not the device address.  Each device's address comes
+// from hipGetSymbolAddress, called once per device with that device current,
+// and is kept in scratch_dev[].
+constexpr size_t kNoAllocScratchBytes = size_t(1) << 20;
+static __device__ __align__(256) int32_t scratch[kNoAllocScratchBytes / sizeof(int32_t)];
+constexpr int kMaxDevices = 64;
+std::atomic<int32_t*> scratch_dev[kMaxDevices];
+std::mutex scratch_mu;
+
+// This device's copy of `scratch` (resolved on the first call on the device).
+int device_scratch(int32_t** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return FMOE_ERR_LAUNCH;
+  int32_t* p = scratch_dev[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    p = scratch_dev[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      void* addr = nullptr;
+      if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || addr == nullptr)
+        return FMOE_ERR_LAUNCH;
+      p = static_cast<int32_t*>(addr);
+      scratch_dev[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return FMOE_OK;
+}
+
+}  // namespace
+
 extern "C" int fmoe_dispatch(const int32_t* idx, const void* x, int64_t T, int64_t dim,
                              int n_experts, int k, int32_t* counts, int32_t* offsets,
                              int32_t* perm, int32_t* pos_of_slot, void* x_perm, void* workspace,
@@ -296,4 +336,20 @@ extern "C" int fmoe_dispatch(const int32_t* idx, const void* x, int64_t T, int64
         perm, static_cast<const uint4*>(x), n_slots, chunks, k, static_cast<uint4*>(x_perm));
   }
   return launch_status();
+}
+
+extern "C" int fmoe_dispatch_noalloc(const int32_t* idx, const void* x, int64_t T, int64_t dim,
+                                     int n_experts, int k, int32_t* counts, int32_t* offsets,
+                                     int32_t* perm, int32_t* pos_of_slot, void* x_perm, void* stream) {
+  if (T < 0 || dim <= 0) return FMOE_ERR_INVALID_ARG;
+  if (n_experts <= 0 || n_experts > FMOE_MAX_EXPERTS) return FMOE_ERR_TOO_MANY_EXPERTS;
+  if (k <= 0 || k > FMOE_MAX_TOPK || k > n_experts || dim % 64 != 0) return FMOE_ERR_SHAPE;
+  if (T * k > INT32_MAX / 2) return FMOE_ERR_SHAPE;
+  const size_t need = fmoe_dispatch_workspace_bytes(T, n_experts, k);
+  if (need > kNoAllocScratchBytes) return FMOE_ERR_SCRATCH;
+  int32_t* ws = nullptr;
+  const int rc = device_scratch(&ws);
+  if (rc != FMOE_OK) return rc;
+  return fmoe_dispatch(idx, x, T, dim, n_experts, k, counts, offsets, perm, pos_of_slot, x_perm, ws,
+                       kNoAllocScratchBytes, stream);
 }

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define FMOE_ABI_VERSION 7
+#define FMOE_ABI_VERSION 8
 #define FMOE_MAX_EXPERTS 64
 #define FMOE_MAX_TOPK 8
 #define FMOE_MAX_CAST 64
@@ -54,7 +54,8 @@ enum fmoe_status {
   FMOE_ERR_DTYPE = 4,         /* unknown dtype code */
   FMOE_ERR_LAUNCH = 5,        /* hipGetLastError after a launch */
   FMOE_ERR_WORKSPACE = 6,     /* workspace smaller than the size query returned */
-  FMOE_ERR_TOO_MANY_EXPERTS = 7
+  FMOE_ERR_TOO_MANY_EXPERTS = 7,
+  FMOE_ERR_SCRATCH = 8        /* workload beyond the static scratch of an allocation-free entry point */
 };
 
 enum fmoe_dtype { FMOE_BF16 = 0, FMOE_F32 = 1 };
@@ -101,6 +102,21 @@ int fmoe_dispatch(const int32_t* idx, const void* x, int64_t T, int64_t dim,
                   int32_t* counts, int32_t* offsets, int32_t* perm,
                   int32_t* pos_of_slot, void* x_perm,
                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* Allocation-free fmoe_dispatch.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP-graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * kernels and outputs as fmoe_dispatch, minus the workspace: the scratch is a
+ * static 1 MiB array in device memory, one per GPU, held until the process
+ * ends.  Workloads with fmoe_dispatch_workspace_bytes(T, E, k) > 1 MiB
+ * (2 * ceil(T*k / 256) * E int32, e.g. T*k above 4.2 M slots at E = 8 or
+ * 524288 slots at E = 64) return FMOE_ERR_SCRATCH.  The scratch needs no
+ * clearing (every call rewrites what it reads).  Calls that overlap on one
+ * GPU (on different streams) share the array and race: order them. */
+int fmoe_dispatch_noalloc(const int32_t* idx, const void* x, int64_t T, int64_t dim,
+                          int n_experts, int k,
+                          int32_t* counts, int32_t* offsets, int32_t* perm,
+                          int32_t* pos_of_slot, void* x_perm, void* stream);
 
 /* Routing and dispatch of a tiny batch (T <= 16 tokens, decode) in one
  * launch: the outputs of fmoe_router_fwd followed by fmoe_dispatch on its idx,

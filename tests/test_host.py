@@ -21,7 +21,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     syms = declared_symbols()
-    assert len(syms) == 24
+    assert len(syms) == 25
     for s in syms:
         assert hasattr(lib, s), s
     assert set(syms) == set(_lib.SIGNATURES), "ctypes binding and header disagree"
@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 def test_status_strings():
     lib = _lib.load()
     assert lib.fmoe_status_string(0) == b"ok"
-    for code in range(1, 8):
+    for code in range(1, 9):
         assert lib.fmoe_status_string(code) != b"unknown status"
     assert lib.fmoe_status_string(99) == b"unknown status"
 
@@ -45,6 +45,14 @@ def test_argument_errors_without_gpu():
     assert lib.fmoe_router_fwd(None, None, None, 4, 768, 8, 9, 1.0, None, None, None, None, None) == 2
     assert lib.fmoe_router_fwd(None, None, None, -1, 768, 8, 2, 1.0, None, None, None, None, None) == 1
     assert lib.fmoe_router_fwd(None, None, None, 4, 768, 8, 2, 1.0, None, None, None, None, None) == 1
+    # the allocation-free dispatch: shape errors as fmoe_dispatch, and a
+    # workload beyond its 1 MiB static scratch (2 * ceil(T*k/256) * E int32)
+    assert lib.fmoe_dispatch_noalloc(None, None, 4, 768, 65, 2, None, None, None, None, None, None) == 7
+    assert lib.fmoe_dispatch_noalloc(None, None, 4, 100, 8, 2, None, None, None, None, None, None) == 2
+    assert lib.fmoe_dispatch_workspace_bytes(87381, 64, 6) <= 1 << 20
+    assert lib.fmoe_dispatch_workspace_bytes(87382, 64, 6) > 1 << 20
+    assert lib.fmoe_dispatch_noalloc(None, None, 87382, 2048, 64, 6, None, None, None, None, None, None) == 8
+    assert b"1 MiB" in lib.fmoe_status_string(8)
     pp = _lib.ptr_array([0])
     assert lib.fmoe_gateup_fwd(None, None, None, 1, 10, 0, 96, 128, pp, pp, None, None, None) == 2
     assert lib.fmoe_gateup_fwd(None, None, None, 1, 10, 0, 128, 128, pp, pp, None, None, None) == 1
