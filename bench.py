@@ -13,9 +13,12 @@ The JSON line also carries:
                 the launch's average duration, timed with HIP events on the
                 stream the kernels run on, inside the timed region (only
                 that entry point carries events there);
-  kernels       the same figures for every entry point of the step, from a
-                short untimed pass with events around every entry point
-                (it also names the dominant one);
+  kernels       the same figures for every entry point of the step: the
+                GEMMs from a short untimed pass with events around every
+                entry point (it also names the dominant one), the
+                HBM-bound routing, dispatch, combine, transpose and reduce
+                entry points from graphs of 20 back-to-back launches (events
+                around such short kernels add their launch gaps);
   cpu_baseline  the reference algorithm (torch-CPU restatement, the oracle)
                 timed on this host's cores on a bounded sample of the same
                 workload.
@@ -152,29 +155,71 @@ def graph_entry_times(m, x, reps=20, replays=20):
         "down_fwd": lambda: K.down_fwd(h, offsets, E, rows_r, rows_s, w2s, d),
         "combine_fwd": lambda: K.combine_fwd(o, idx, w, pos, rows_r, has_shared, x.dtype, None),
     })
-    out = {}
-    for name, fn in calls.items():
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            for _ in range(2):
-                fn()
-        torch.cuda.current_stream().wait_stream(side)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for _ in range(reps):
-                fn()
+    return {name: graph_time(fn, reps, replays) for name, fn in calls.items()}
+
+
+def graph_time(fn, reps=20, replays=20):
+    """Per-launch time (us) of fn: a HIP graph of `reps` back-to-back calls,
+    replayed `replays` times between two HIP events on the replaying stream
+    (no event between the launches, so short kernels are not inflated)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(replays):
         g.replay()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(replays):
-            g.replay()
-        b.record()
-        torch.cuda.synchronize()
-        out[name] = a.elapsed_time(b) * 1e3 / (reps * replays)
-        del g
-    return out
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / (reps * replays)
+    del g
+    return us
+
+
+def graph_hbm_times(m, x, dy):
+    """Per-launch time (us) of the HBM-bound entry points of one forward +
+    backward of the DeepSeekMoE block (routing, dispatch, combine and their
+    backward, the transposed weight copies), each from a graph of
+    back-to-back launches on the workload's own intermediates (graph_time).
+    Events around every call of an eager step inflate such short kernels by
+    their launch gaps; this is the figure the roofline fractions of these
+    kernels use."""
+    from fusionllm_amd import _kernels as K
+    from fusionllm_amd.moe import _forward_pass
+    E, k = m.n_routed_experts, m.n_activated_experts
+    has_shared = m.shared_expert is not None
+    rs = float(m.route_scale)
+    meta = (E, k, m.moe_inter_dim, rs, has_shared, x.dtype)
+    with torch.no_grad():
+        fw = _forward_pass(meta, x, m.gate.weight, m.gate.bias, m._flat_weights())
+        xb, gwb, wb, idx, idx64, w, v, counts, offsets, perm, pos, x_perm, ab, h, o, y = fw
+        T, d = xb.shape
+        G = E + (1 if has_shared else 0)
+        w1s, w3s, w2s = wb[0::3][:G], wb[1::3][:G], wb[2::3][:G]
+        gbb = m.gate.bias.to(torch.bfloat16).contiguous()
+        dyb = dy.to(torch.bfloat16).contiguous()
+        d_o, d_w = K.combine_bwd(dyb, o, w, perm, k)
+        d_logits, _, _ = K.router_bwd(d_w, v, perm, offsets, x_perm, E, rs, m.gate.weight.dtype)
+        dx_rows = torch.empty(o.shape, dtype=torch.bfloat16, device=o.device).normal_()
+        calls = {
+            "router_fwd": lambda: K.router_fwd(xb, gwb, gbb, k, rs),
+            "dispatch": lambda: K.dispatch(idx, xb, E),
+            "combine_fwd": lambda: K.combine_fwd(o, idx, w, pos, T * k, has_shared, x.dtype, None),
+            "combine_bwd": lambda: K.combine_bwd(dyb, o, w, perm, k),
+            "router_bwd": lambda: K.router_bwd(d_w, v, perm, offsets, x_perm, E, rs, m.gate.weight.dtype),
+            "dx_reduce": lambda: K.dx_reduce(dx_rows, pos, idx, d_logits, gwb, T * k, has_shared, x.dtype),
+            "transpose_weights": lambda: K.transpose_weights(w1s, w3s, w2s),
+        }
+        return {name: graph_time(fn) for name, fn in calls.items()}
 
 
 def hbm_traffic(cfg_name, entry):
@@ -539,6 +584,14 @@ def main():
         dom = max(kernels, key=lambda n: kernels[n]["share"])
         timer = {}
     dk = (table_of(timer, args.steps, elapsed) if timer else kernels)[dom]
+    if not args.fwd_only and not norms and not args.autocast:
+        # the HBM-bound entry points from graphs of back-to-back launches
+        step_us = elapsed / args.steps * 1e6
+        for name, us in graph_hbm_times(mods[0], x.detach(), dy).items():
+            bound, work = model[name]
+            kernels[name] = {"avg_us": round(us, 2), "calls": "graph x20", "share": round(us / step_us, 4),
+                             "bound": "hbm", "achieved_gbs": round(work / (us / 1e6) / 1e9, 1),
+                             "frac": round(work / (us / 1e6) / PEAK_HBM_BYTES, 4)}
 
     bound, work = model[dom]
     avg_s = dk["avg_us"] / 1e6
