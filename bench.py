@@ -115,6 +115,9 @@ def kernel_model(cfg, T, active_groups=None):
         "combine_fwd": ("hbm", T * (k * 2 * d + 2 * d + 8 * k + 4 * k + 2 * d)),
         "combine_bwd": ("hbm", T * k * (2 * d + 2 * d + 2 * d + 4 + 4 + 4)),
         "router_bwd": ("hbm", T * k * (2 * d + 4 * 4)),
+        # routing + dispatch in one entry point: x read once; idx, idx64, weights, scores,
+        # perm, pos and the k rows of x_perm written
+        "route_and_dispatch": ("hbm", T * (2 * d + 4 * k + 8 * k + 4 * k + 4 * k + 4 * k + 4 * k + k * 2 * d)),
         "dx_reduce": ("hbm", T * (k * 2 * d + 2 * d + 2 * d + 12 * k)),
         # C4 (RMSNorm + MoE + residual): x in, xn and rstd out; the backward
         # reads the k routed + shared rows, x and d_out and writes dx
@@ -216,6 +219,7 @@ def graph_hbm_times(m, x, dy):
             "combine_fwd": lambda: K.combine_fwd(o, idx, w, pos, T * k, has_shared, x.dtype, None),
             "combine_bwd": lambda: K.combine_bwd(dyb, o, w, perm, k),
             "router_bwd": lambda: K.router_bwd(d_w, v, perm, offsets, x_perm, E, rs, m.gate.weight.dtype),
+            "route_and_dispatch": lambda: K.route_and_dispatch(xb, gwb, gbb, k, rs),
             "dx_reduce": lambda: K.dx_reduce(dx_rows, pos, idx, d_logits, gwb, T * k, has_shared, x.dtype),
             "transpose_weights": lambda: K.transpose_weights(w1s, w3s, w2s),
         }

@@ -122,6 +122,36 @@ def route_dispatch(x, gate_w, gate_b, k: int, route_scale: float):
 
 
 @_timed
+def route_and_dispatch(x, gate_w, gate_b, k: int, route_scale: float, gather: bool = True):
+    """router_fwd followed by dispatch for any T, in three launches (the router counts the
+    dispatch histogram, the scatter copies the rows); returns idx32, idx64, weights, topv,
+    counts, offsets, perm, pos, x_perm."""
+    lib = _lib.load()
+    T, d = x.shape
+    E = gate_w.shape[0]
+    dev = x.device
+    idx = torch.empty(T, k, dtype=torch.int32, device=dev)
+    idx64 = torch.empty(T, k, dtype=torch.int64, device=dev)
+    w = torch.empty(T, k, dtype=torch.float32, device=dev)
+    v = torch.empty(T, k, dtype=torch.float32, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(T * k, dtype=torch.int32, device=dev)
+    pos = torch.empty(T * k, dtype=torch.int32, device=dev)
+    x_perm = torch.empty(T * k, d, dtype=torch.bfloat16, device=dev) if gather else None
+    ws_bytes = lib.fmoe_route_and_dispatch_workspace_bytes(T, E, k)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    check(lib.fmoe_route_and_dispatch(_req(x, "x", torch.bfloat16), _req(gate_w, "gate.weight", torch.bfloat16),
+                                      _req(gate_b, "gate.bias", torch.bfloat16), T, d, E, k, float(route_scale),
+                                      idx.data_ptr(), idx64.data_ptr(), w.data_ptr(), v.data_ptr(),
+                                      counts.data_ptr(), offsets.data_ptr(), perm.data_ptr(), pos.data_ptr(),
+                                      x_perm.data_ptr() if x_perm is not None else None,
+                                      ws.data_ptr(), ws_bytes, _stream()),
+          "fmoe_route_and_dispatch")
+    return idx, idx64, w, v, counts, offsets, perm, pos, x_perm
+
+
+@_timed
 def dispatch(idx, x, n_experts: int, gather: bool = True, noalloc: bool = False):
     """Histogram + scan + stable scatter (+ row gather); returns counts, offsets, perm, pos, x_perm.
     noalloc: fmoe_dispatch_noalloc, whose scratch is the library's static device array."""

@@ -51,9 +51,15 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_hist_kernel(
 // block_base[b][e] = offsets[e] + sum_{b' < b} block_hist[b'][e]: pass 1 adds
 // each expert's block counts (wave reduction), thread 0 turns the totals into
 // offsets, pass 2 writes the per-block bases with a 64-lane inclusive scan
-// (shfl_up) per chunk of 64 blocks, carried across chunks.  Integer sums, so
-// the order does not change the result.
+// (shfl_up) per chunk of 64 blocks, carried across chunks.  When the block
+// counts fit (nblocks * E <= kScanStaged) they are first copied to LDS with
+// every thread's loads in flight at once; with at most 16 experts and 1024
+// blocks the two passes then become one (a lane per run of blocks, one
+// 64-lane scan per expert).  Integer sums, so the order does not change the
+// result.
 constexpr int kScanThreads = 1024;
+constexpr int kScanStaged = 12288;  // 48 KB of LDS
+constexpr int kScanRun = 16;        // one-pass path: up to 64 * 16 blocks, one expert per wave
 
 __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 #pragma unroll
@@ -69,11 +75,74 @@ __global__ __launch_bounds__(kScanThreads) void dispatch_scan_kernel(
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets) {
   __shared__ int total[FMOE_MAX_EXPERTS];
   __shared__ int start[FMOE_MAX_EXPERTS + 1];
+  __shared__ int hsh[kScanStaged];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   constexpr int nwaves = kScanThreads / 64;
+  const int n = nblocks * E;
+  const bool staged = n <= kScanStaged;  // uniform over the workgroup
+  if (staged) {
+    int hv[kScanStaged / kScanThreads];  // every load issued before the first LDS store
+#pragma unroll
+    for (int u = 0; u < kScanStaged / kScanThreads; ++u) {
+      const int i = threadIdx.x + u * kScanThreads;
+      hv[u] = i < n ? block_hist[i] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kScanStaged / kScanThreads; ++u) {
+      const int i = threadIdx.x + u * kScanThreads;
+      if (i < n) hsh[i] = hv[u];
+    }
+    __syncthreads();
+  }
+  const int* src = staged ? hsh : block_hist;
+  if (staged && E <= nwaves && nblocks <= 64 * kScanRun) {
+    // One pass: wave e takes expert e; lane l owns the run of blocks
+    // [l * run, (l + 1) * run), kept in registers.  A 64-lane scan of the run
+    // sums gives each run's first base and the expert's total.
+    const int run = (nblocks + 63) / 64;
+    const int e = wave;
+    int hv[kScanRun];
+    int loc = 0;
+#pragma unroll
+    for (int j = 0; j < kScanRun; ++j) {
+      const int b = lane * run + j;
+      hv[j] = (e < E && j < run && b < nblocks) ? hsh[b * E + e] : 0;
+      loc += hv[j];
+    }
+    const int incl = wave_incl_scan(loc, lane);
+    if (e < E && lane == 63) total[e] = incl;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int acc = 0;
+      for (int q = 0; q < E; ++q) { start[q] = acc; acc += total[q]; }
+      start[E] = acc;
+    }
+    __syncthreads();
+    for (int q = threadIdx.x; q < E; q += kScanThreads) {
+      counts[q] = total[q];
+      offsets[q] = start[q];
+    }
+    if (threadIdx.x == 0) offsets[E] = start[E];
+    // bases to LDS (over the staged counts, all read by now), then copied out coalesced
+    __syncthreads();
+    if (e < E) {
+      int base = start[e] + incl - loc;
+#pragma unroll
+      for (int j = 0; j < kScanRun; ++j) {
+        const int b = lane * run + j;
+        if (j < run && b < nblocks) {
+          hsh[b * E + e] = base;
+          base += hv[j];
+        }
+      }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += kScanThreads) block_base[i] = hsh[i];
+    return;
+  }
   for (int e = wave; e < E; e += nwaves) {
     int sum = 0;
-    for (int b = lane; b < nblocks; b += 64) sum += block_hist[static_cast<int64_t>(b) * E + e];
+    for (int b = lane; b < nblocks; b += 64) sum += src[static_cast<int64_t>(b) * E + e];
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
     if (lane == 0) total[e] = sum;
@@ -95,7 +164,7 @@ __global__ __launch_bounds__(kScanThreads) void dispatch_scan_kernel(
     for (int b0 = 0; b0 < nblocks; b0 += 64) {
       const int b = b0 + lane;
       const int64_t o = static_cast<int64_t>(b) * E + e;
-      const int h = b < nblocks ? block_hist[o] : 0;
+      const int h = b < nblocks ? src[o] : 0;
       const int incl = wave_incl_scan(h, lane);
       if (b < nblocks) block_base[o] = carry + incl - h;
       carry += __shfl(incl, 63, 64);
@@ -147,6 +216,76 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_scatter_kernel(
       running[q] += add;
     }
     __syncthreads();
+  }
+}
+
+// fmoe_route_and_dispatch's scatter: workgroup (b, y) takes the slots of the
+// router's workgroup b (kRouteBlockTokens tokens, spb = kRouteBlockTokens * k
+// <= 256 slots, one per thread) and ranks them exactly as
+// dispatch_scatter_kernel does (ballots within a wave, then the counts of the
+// earlier waves); y == 0 writes perm and pos_of_slot.  Every y then copies its
+// share of the block's token rows: the block's tokens * chunks 16-byte chunks
+// cut into ranges of kCopyPerWG, range y for workgroup y, one chunk per
+// thread, each chunk of x read once and stored to the k rows of x_perm its
+// token's slots go to.  Re-ranking in every y costs a few ballots; it buys
+// enough workgroups to keep the copy's loads in flight.
+constexpr int kCopyPerWG = kDispThreads;
+
+__global__ __launch_bounds__(kDispThreads) void dispatch_scatter_copy_kernel(
+    const int32_t* __restrict__ idx, int n_slots, int spb, int E, int k, const int32_t* __restrict__ block_base,
+    const uint4* __restrict__ x, int chunks, int32_t* __restrict__ perm, int32_t* __restrict__ pos_of_slot,
+    uint4* __restrict__ x_perm) {
+  __shared__ int wcount[kDispWaves][FMOE_MAX_EXPERTS];
+  __shared__ int base_sh[FMOE_MAX_EXPERTS];
+  __shared__ int pos_sh[kDispThreads];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int s0 = blockIdx.x * spb;
+  const int s = s0 + threadIdx.x;
+  const bool mine = threadIdx.x < spb && s < n_slots;
+  // the slot's expert and the block's bases are loaded side by side
+  const int e_raw = mine ? idx[s] : -1;
+  const int bb = threadIdx.x < E ? block_base[static_cast<int64_t>(blockIdx.x) * E + threadIdx.x] : 0;
+  for (int i = threadIdx.x; i < kDispWaves * E; i += blockDim.x) wcount[i / E][i % E] = 0;
+  if (threadIdx.x < E) base_sh[threadIdx.x] = bb;
+  __syncthreads();
+  const bool valid = static_cast<unsigned>(e_raw) < static_cast<unsigned>(E);
+  const int e = valid ? e_raw : -1;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  uint64_t pending = __ballot(valid);
+  int rank = 0;
+  while (pending) {
+    const int leader = __ffsll(static_cast<unsigned long long>(pending)) - 1;
+    const int le = __shfl(e, leader);
+    const uint64_t m = __ballot(e == le);
+    if (e == le) rank = __popcll(m & lt_mask);
+    if (lane == leader) wcount[wave][le] = __popcll(m);
+    pending &= ~m;
+  }
+  __syncthreads();
+  int pos = -1;
+  if (valid) {
+    pos = base_sh[e] + rank;
+    for (int w = 0; w < wave; ++w) pos += wcount[w][e];
+    if (pos < 0 || pos >= n_slots) pos = -1;  // never, for expert ids in range
+    if (pos >= 0 && blockIdx.y == 0) {
+      perm[pos] = s;
+      pos_of_slot[s] = pos;
+    }
+  }
+  if (x_perm == nullptr) return;
+  if (threadIdx.x < spb) pos_sh[threadIdx.x] = pos;
+  __syncthreads();
+  const int t0 = s0 / k;                       // the block's first token (spb is a multiple of k)
+  const int ntok = min(spb, n_slots - s0) / k;  // n_slots = T * k: whole tokens
+  const int g = blockIdx.y * kCopyPerWG + threadIdx.x;
+  if (g < ntok * chunks) {
+    const int i = g / chunks, c = g - i * chunks;
+    const uint4 v = x[static_cast<int64_t>(t0 + i) * chunks + c];
+    for (int j = 0; j < k; ++j) {
+      const int p = pos_sh[i * k + j];
+      if (p >= 0) x_perm[static_cast<int64_t>(p) * chunks + c] = v;
+    }
   }
 }
 
@@ -352,4 +491,46 @@ extern "C" int fmoe_dispatch_noalloc(const int32_t* idx, const void* x, int64_t 
   if (rc != FMOE_OK) return rc;
   return fmoe_dispatch(idx, x, T, dim, n_experts, k, counts, offsets, perm, pos_of_slot, x_perm, ws,
                        kNoAllocScratchBytes, stream);
+}
+
+extern "C" size_t fmoe_route_and_dispatch_workspace_bytes(int64_t T, int n_experts, int k) {
+  if (T <= 0 || n_experts <= 0 || k <= 0) return 0;
+  const int64_t nblocks = ceil_div(T, kRouteBlockTokens);
+  return static_cast<size_t>(2 * nblocks * n_experts) * sizeof(int32_t);  // block counts, block bases
+}
+
+extern "C" int fmoe_route_and_dispatch(const void* x, const void* gate_w, const void* gate_b, int64_t T,
+                                       int64_t dim, int n_experts, int k, float route_scale, int32_t* idx,
+                                       int64_t* idx64, float* weights, float* topv, int32_t* counts,
+                                       int32_t* offsets, int32_t* perm, int32_t* pos_of_slot, void* x_perm,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+  if (T < 0 || dim <= 0) return FMOE_ERR_INVALID_ARG;
+  if (n_experts <= 0 || n_experts > FMOE_MAX_EXPERTS) return FMOE_ERR_TOO_MANY_EXPERTS;
+  if (k <= 0 || k > FMOE_MAX_TOPK || k > n_experts || dim % 64 != 0 || dim > 2048) return FMOE_ERR_SHAPE;
+  if (T * k > INT32_MAX / 2) return FMOE_ERR_SHAPE;
+  if (!counts || !offsets) return FMOE_ERR_INVALID_ARG;
+  hipStream_t s = as_stream(stream);
+  if (T == 0) {
+    // no tokens: empty experts (the scan over zero blocks writes counts 0, offsets 0)
+    dispatch_scan_kernel<<<1, kScanThreads, 0, s>>>(nullptr, 0, n_experts, nullptr, counts, offsets);
+    return launch_status();
+  }
+  if (!x || !gate_w || !gate_b || !idx || !weights || !topv || !perm || !pos_of_slot) return FMOE_ERR_INVALID_ARG;
+  if (!aligned16(x) || !aligned16(gate_w) || (x_perm && !aligned16(x_perm))) return FMOE_ERR_ALIGN;
+  if (workspace_bytes < fmoe_route_and_dispatch_workspace_bytes(T, n_experts, k)) return FMOE_ERR_WORKSPACE;
+  if (!workspace) return FMOE_ERR_INVALID_ARG;
+  const int64_t nblocks = ceil_div(T, kRouteBlockTokens);
+  int32_t* block_hist = static_cast<int32_t*>(workspace);
+  int32_t* block_base = block_hist + nblocks * n_experts;
+  int st = launch_router_hist(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(gate_w),
+                              static_cast<const uint16_t*>(gate_b), T, dim, n_experts, k, route_scale, idx, idx64,
+                              weights, topv, block_hist, s);
+  if (st) return st;
+  dispatch_scan_kernel<<<1, kScanThreads, 0, s>>>(block_hist, static_cast<int>(nblocks), n_experts, block_base,
+                                                   counts, offsets);
+  const int64_t nsplit = x_perm ? ceil_div(static_cast<int64_t>(kRouteBlockTokens) * (dim / 8), kCopyPerWG) : 1;
+  dispatch_scatter_copy_kernel<<<dim3(nblocks, nsplit), dim3(kDispThreads), 0, s>>>(
+      idx, static_cast<int>(T * k), kRouteBlockTokens * k, n_experts, k, block_base,
+      static_cast<const uint4*>(x), static_cast<int>(dim / 8), perm, pos_of_slot, static_cast<uint4*>(x_perm));
+  return launch_status();
 }

@@ -113,4 +113,11 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Tokens per router workgroup, which are also the dispatch blocks of
+// fmoe_route_and_dispatch; and its routing launch (router.hip).
+constexpr int kRouteBlockTokens = 32;
+int launch_router_hist(const uint16_t* xs, const uint16_t* ws, const uint16_t* bs, int64_t T, int64_t dim,
+                       int n_experts, int k, float route_scale, int32_t* idx, int64_t* idx64, float* weights,
+                       float* topv, int32_t* block_hist, hipStream_t s);
+
 }  // namespace fmoe

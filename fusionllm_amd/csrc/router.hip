@@ -17,15 +17,21 @@
 namespace fmoe {
 
 constexpr int kRouterLanes = 16;
-constexpr int kRouterTok = 32;       // tokens per workgroup (32 x 16 lanes = 512 threads)
+constexpr int kRouterTok = kRouteBlockTokens;  // tokens per workgroup
+constexpr int kRouterPerGroup = 1;             // tokens per 16-lane group
+constexpr int kRouterThreads = kRouterTok / kRouterPerGroup * kRouterLanes;
 constexpr int kRouterEBlk = 8;       // experts whose gate rows sit in LDS at a time (fp32: 64 KB at dim 2048)
-constexpr int kRouterMaxDim = 2048;  // a lane keeps its <= 16 x chunks in registers
+constexpr int kRouterMaxDim = 2048;  // a lane keeps its <= 16 x chunks per token in registers
 
-// One workgroup routes 32 tokens.  The gate rows are staged in LDS, 16
-// experts at a time, so the gate matrix is read from memory once per 32
+// One workgroup routes 32 tokens.  The gate rows are staged in LDS as fp32,
+// 8 experts at a time, so the gate matrix is read from memory once per 32
 // tokens instead of once per token; each lane keeps its x chunks in
-// registers across the expert blocks.  The logits (without bias) go to LDS
-// and every lane of a token's group then computes the scores and the top-k.
+// registers across the expert blocks.  (The kernel can give each 16-lane
+// group R tokens, every gate chunk read from LDS feeding all R; measured at
+// dim 768 with 8 experts, R = 2 is slower than R = 1: half the waves, each
+// with twice the FMA chains.)  The logits (without bias) go to LDS; the
+// scores are computed once per (token, expert), spread over the group's
+// lanes, and every lane of a token's group then takes the top-k.
 // Lane l gets v from lane l ^ off (off < 16): ds_swizzle in xor mode, within
 // groups of 32 lanes.
 __device__ __forceinline__ float xor_lane(float v, int off) {
@@ -39,19 +45,17 @@ __device__ __forceinline__ float xor_lane(float v, int off) {
   return __int_as_float(r);
 }
 
-// Scores and top-k of one token from its logits lg[0 .. E) (bias not yet
-// added), computed redundantly by the 16 lanes of the token's group; lane
-// j < k writes the j-th choice.
-template <int EB>
-__device__ __forceinline__ void route_token(const float* lg, const uint16_t* __restrict__ bg, int E, int k,
-                                            float route_scale, int lane16, bool active, int t,
-                                            int32_t* __restrict__ idx, int64_t* __restrict__ idx64,
-                                            float* __restrict__ wout, float* __restrict__ vout,
-                                            int* idx_lds = nullptr) {
-  float s[EB];
-#pragma unroll
-  for (int e = 0; e < EB; ++e) s[e] = (e < E) ? fm_sigmoid(lg[e] + bf2f(bg[e])) : 0.0f;
+// Gate bias of expert e: bf16 in memory, or already converted to fp32 (LDS).
+__device__ __forceinline__ float bias_at(const uint16_t* __restrict__ b, int e) { return bf2f(b[e]); }
+__device__ __forceinline__ float bias_at(const float* b, int e) { return b[e]; }
 
+// Top-k of one token from its scores s[0 .. E), computed redundantly by the
+// 16 lanes of the token's group; lane j < k writes the j-th choice.
+template <int EB>
+__device__ __forceinline__ void pick_topk(const float (&s)[EB], int E, int k, float route_scale, int lane16,
+                                          bool active, int t, int32_t* __restrict__ idx,
+                                          int64_t* __restrict__ idx64, float* __restrict__ wout,
+                                          float* __restrict__ vout, int* idx_lds, int* hist_lds) {
   // k selection rounds (a runtime loop over the token's k); lane j keeps the
   // j-th choice, and the chosen scores are summed in choice order.
   uint64_t taken = 0;
@@ -78,63 +82,121 @@ __device__ __forceinline__ void route_token(const float* lg, const uint16_t* __r
     if (idx64) idx64[o] = e_sel;
     wout[o] = (v_sel / denom) * route_scale;
     vout[o] = v_sel;
+    if (hist_lds) atomicAdd(&hist_lds[e_sel], 1);  // integer count: exact in any order
   }
 }
 
-template <int EB, int NQ>  // NQ: x chunks per lane, NQ * 16 * 8 >= dim
-__global__ __launch_bounds__(512) void router_fwd_kernel(
+// Scores and top-k of one token from its logits lg[0 .. E) (bias not yet
+// added), the scores also computed redundantly by the group's 16 lanes.
+template <int EB, typename BiasT>
+__device__ __forceinline__ void route_token(const float* lg, const BiasT* bg, int E, int k,
+                                            float route_scale, int lane16, bool active, int t,
+                                            int32_t* __restrict__ idx, int64_t* __restrict__ idx64,
+                                            float* __restrict__ wout, float* __restrict__ vout,
+                                            int* idx_lds = nullptr, int* hist_lds = nullptr) {
+  float s[EB];
+#pragma unroll
+  for (int e = 0; e < EB; ++e) s[e] = (e < E) ? fm_sigmoid(lg[e] + bias_at(bg, e)) : 0.0f;
+  pick_topk<EB>(s, E, k, route_scale, lane16, active, t, idx, idx64, wout, vout, idx_lds, hist_lds);
+}
+
+template <int EB, int NQ, int R>  // NQ: x chunks per lane, NQ * 16 * 8 >= dim; R tokens per group
+// block_hist (nullable): the workgroup's choices counted per expert,
+// block_hist[blockIdx.x * E + e] — the histogram stage of the dispatch for
+// blocks of kRouterTok tokens (used by fmoe_route_and_dispatch).
+// Group g (16 lanes) takes tokens g, g + 32 / R, ... of the workgroup's 32.
+// The first expert block's gate loads are issued before the x loads, so that
+// staging them (which waits for its loads, and memory loads return in issue
+// order) does not wait for x.
+__global__ __launch_bounds__(kRouterTok / R * kRouterLanes) void router_fwd_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg,
     const uint16_t* __restrict__ bg, int T, int dim, int E, int k, float route_scale,
     int32_t* __restrict__ idx, int64_t* __restrict__ idx64, float* __restrict__ wout,
-    float* __restrict__ vout) {
+    float* __restrict__ vout, int32_t* __restrict__ block_hist) {
   constexpr int EBLK = EB < kRouterEBlk ? EB : kRouterEBlk;  // experts per LDS block
+  constexpr int NG = kRouterTok / R;                          // groups per workgroup
+  constexpr int NT = NG * kRouterLanes;                       // threads
+  constexpr int GMAX = (EBLK * NQ * kRouterLanes + NT - 1) / NT;  // gate chunks per thread and block
   // Gate rows converted to fp32 once per workgroup, each 8-element chunk as
   // two float4 planes (elements 0-3, 4-7): consecutive lanes read consecutive
   // 16-byte words, and no lane unpacks bf16 per token.
   __shared__ float4 wlo[EBLK * NQ * kRouterLanes];
   __shared__ float4 whi[EBLK * NQ * kRouterLanes];
   __shared__ float lsh[kRouterTok * EB];
+  __shared__ float bsh[EB];
+  __shared__ int hcnt[EB];
+  if (block_hist != nullptr && threadIdx.x < EB) hcnt[threadIdx.x] = 0;  // ordered by the first barrier below
   const int lane16 = threadIdx.x % kRouterLanes;
-  const int tl = threadIdx.x / kRouterLanes;
-  const int t = blockIdx.x * kRouterTok + tl;
-  const bool active = t < T;
-  const int tc = active ? t : T - 1;  // idle lanes route a copy of the last token
+  const int grp = threadIdx.x / kRouterLanes;
   const int nchunk = dim / 8;
 
-  const uint4* xrow = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(tc) * dim);
-  uint4 xr[NQ];
+  uint4 gr[GMAX];
+  auto load_gate = [&](int e0, int ne) {
+    const uint4* src = reinterpret_cast<const uint4*>(wg + static_cast<int64_t>(e0) * dim);
 #pragma unroll
-  for (int q = 0; q < NQ; ++q) {
-    const int c = lane16 + kRouterLanes * q;
-    xr[q] = c < nchunk ? xrow[c] : make_uint4(0, 0, 0, 0);
+    for (int u = 0; u < GMAX; ++u) {
+      const int i = threadIdx.x + u * NT;
+      gr[u] = i < ne * nchunk ? src[i] : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store_gate = [&](int ne) {
+#pragma unroll
+    for (int u = 0; u < GMAX; ++u) {
+      const int i = threadIdx.x + u * NT;
+      if (i < ne * nchunk) {
+        float f[8];
+        unpack8(gr[u], f);
+        wlo[i] = make_float4(f[0], f[1], f[2], f[3]);
+        whi[i] = make_float4(f[4], f[5], f[6], f[7]);
+      }
+    }
+  };
+  load_gate(0, min(EBLK, E));
+  const float bias = threadIdx.x < E ? bf2f(bg[threadIdx.x]) : 0.0f;
+
+  uint4 xr[R][NQ];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int t = blockIdx.x * kRouterTok + grp + r * NG;
+    const int tc = t < T ? t : T - 1;  // idle lanes route a copy of the last token
+    const uint4* xrow = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(tc) * dim);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int c = lane16 + kRouterLanes * q;
+      xr[r][q] = c < nchunk ? xrow[c] : make_uint4(0, 0, 0, 0);
+    }
   }
+  if (threadIdx.x < E) bsh[threadIdx.x] = bias;  // ordered by the first barrier below
 
   for (int e0 = 0; e0 < E; e0 += EBLK) {
     const int ne = min(EBLK, E - e0);
-    __syncthreads();  // the previous block's gate rows are no longer read
-    for (int i = threadIdx.x; i < ne * nchunk; i += blockDim.x) {
-      float f[8];
-      unpack8(reinterpret_cast<const uint4*>(wg + static_cast<int64_t>(e0) * dim)[i], f);
-      wlo[i] = make_float4(f[0], f[1], f[2], f[3]);
-      whi[i] = make_float4(f[4], f[5], f[6], f[7]);
+    if (e0 > 0) {
+      __syncthreads();  // the previous block's gate rows are no longer read
+      load_gate(e0, ne);
     }
+    store_gate(ne);
     __syncthreads();
-    float acc[EBLK];
+    float acc[R][EBLK];
 #pragma unroll
-    for (int e = 0; e < EBLK; ++e) acc[e] = 0.0f;
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int e = 0; e < EBLK; ++e) acc[r][e] = 0.0f;
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int c = lane16 + kRouterLanes * q;
       if (c < nchunk) {
-        float xf[8];
-        unpack8(xr[q], xf);
+        float xf[R][8];
+#pragma unroll
+        for (int r = 0; r < R; ++r) unpack8(xr[r][q], xf[r]);
 #pragma unroll
         for (int e = 0; e < EBLK; ++e) {
           if (e < ne) {
             const float4 a = wlo[e * nchunk + c], b = whi[e * nchunk + c];
             const float wf[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[e] = fmaf(xf[i], wf[i], acc[e]);
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+              for (int i = 0; i < 8; ++i) acc[r][e] = fmaf(xf[r][i], wf[i], acc[r][e]);
           }
         }
       }
@@ -142,16 +204,41 @@ __global__ __launch_bounds__(512) void router_fwd_kernel(
 #pragma unroll
     for (int off = kRouterLanes / 2; off >= 1; off >>= 1) {
 #pragma unroll
-      for (int e = 0; e < EBLK; ++e) acc[e] = acc[e] + xor_lane(acc[e], off);
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int e = 0; e < EBLK; ++e) acc[r][e] = acc[r][e] + xor_lane(acc[r][e], off);
     }
     // every lane now holds the block's logits; lane e writes expert e0 + e
 #pragma unroll
-    for (int e = 0; e < EBLK; ++e)
-      if (e == lane16 && e < ne) lsh[tl * EB + e0 + e] = acc[e];
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int e = 0; e < EBLK; ++e)
+        if (e == lane16 && e < ne) lsh[(grp + r * NG) * EB + e0 + e] = acc[r][e];
   }
   __syncthreads();
 
-  route_token<EB>(lsh + tl * EB, bg, E, k, route_scale, lane16, active, t, idx, idx64, wout, vout);
+  // scores: lane j of a group computes experts j, j + 16, ... of its tokens
+  // (in place over the logits), then every lane reads all E of its token
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float* lg = lsh + (grp + r * NG) * EB;
+    for (int e = lane16; e < E; e += kRouterLanes) lg[e] = fm_sigmoid(lg[e] + bsh[e]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int tl = grp + r * NG;
+    const int t = blockIdx.x * kRouterTok + tl;
+    float sc[EB];
+#pragma unroll
+    for (int e = 0; e < EB; ++e) sc[e] = (e < E) ? lsh[tl * EB + e] : 0.0f;
+    pick_topk<EB>(sc, E, k, route_scale, lane16, t < T, t, idx, idx64, wout, vout, nullptr,
+                  block_hist != nullptr ? hcnt : nullptr);
+  }
+  if (block_hist != nullptr) {
+    __syncthreads();
+    if (threadIdx.x < E) block_hist[static_cast<int64_t>(blockIdx.x) * E + threadIdx.x] = hcnt[threadIdx.x];
+  }
 }
 
 // Decode-sized batches (T <= kRouterSmallT): one workgroup per token and one
@@ -333,19 +420,10 @@ __global__ __launch_bounds__(kTinyThreads) void route_dispatch_tiny_kernel(
 //   dq_j = dw_j * rs;  dv_j = dq_j / D + dS,  dS = -sum_j dq_j * v_j / D^2;
 // top-k backward routes dv_j to the selected score; sigmoid backward gives
 //   dlogit_j = dv_j * (1 - v_j) * v_j.
-// One thread per expert-contiguous row r (slot perm[r] = t*k + j): the
-// normalisation and sigmoid backward of that slot, written by slot (for the
-// input gradient) and by row (for the gate reduction below, which then reads
-// it contiguously).  The token's sums run over j in ascending order.
-__global__ __launch_bounds__(256) void router_dlogit_kernel(
-    const float* __restrict__ dw, const float* __restrict__ v, const int32_t* __restrict__ perm,
-    int n_rows, int k, float rs, float* __restrict__ dl, float* __restrict__ dl_row) {
-  const int r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= n_rows) return;
-  const int slot = perm[r];
-  const int t = slot / k, jr = slot - t * k;
-  const float* dwt = dw + static_cast<int64_t>(t) * k;
-  const float* vt = v + static_cast<int64_t>(t) * k;
+// The normalisation and sigmoid backward of slot t*k + jr, the token's sums
+// taken over j in ascending order.
+__device__ __forceinline__ float slot_dlogit(const float* __restrict__ dwt, const float* __restrict__ vt, int k,
+                                             int jr, float rs) {
   float sum = vt[0];
   for (int j = 1; j < k; ++j) sum = sum + vt[j];
   const float D = sum + 1e-10f;
@@ -356,63 +434,93 @@ __global__ __launch_bounds__(256) void router_dlogit_kernel(
   }
   const float dq = dwt[jr] * rs;
   const float dv = dq / D + dS;
-  const float g = (dv * (1.0f - vt[jr])) * vt[jr];
-  dl[slot] = g;
-  dl_row[r] = g;
+  return (dv * (1.0f - vt[jr])) * vt[jr];
 }
 
 // Gate weight/bias gradient as a segmented column reduction over the
 // expert-contiguous rows:  dWg[e] = sum_{r in e} dl_row[r] * x_perm[r],
-// dbg[e] = sum_{r in e} dl_row[r].  Expert e's rows are cut into
-// ceil(M_e / kChunkRows) chunks, numbered consecutively over the experts
-// (chunk_base(e) = sum of the chunk counts of experts < e).  Stage 1: one
-// block per chunk reduces its rows into partial[chunk][dim+1], row by row in
-// order (loads issued 8 rows at a time).  Stage 2 adds the chunks of each
+// dbg[e] = sum_{r in e} dl_row[r], where dl_row[r] is the logit gradient of
+// slot perm[r].  Expert e's rows are cut into ceil(M_e / kChunkRows) chunks,
+// numbered consecutively over the experts (chunk_base(e) = sum of the chunk
+// counts of experts < e).  Stage 1: one block per chunk reads the E + 1
+// offsets once (into LDS), issues its first kPartialBatch row loads, forms
+// the logit gradients of its rows (one thread per row, also
+// written to d_logits by slot), then reduces its rows into
+// partial[chunk][dim+1], row by row in order (loads issued kPartialBatch rows
+// at a time).  Stage 2 adds the chunks of each
 // expert in chunk order.  Both orders are fixed.
 constexpr int kChunkRows = 32;
+constexpr int kPartialBatch = 16;
 
-__device__ __forceinline__ int expert_chunks(const int32_t* offsets, int e) {
-  return (offsets[e + 1] - offsets[e] + kChunkRows - 1) / kChunkRows;
-}
+constexpr int kPartialThreads = 128;
 
-__global__ __launch_bounds__(128) void router_wgrad_partial_kernel(
-    const float* __restrict__ dl_row, const int32_t* __restrict__ offsets, int E,
+__global__ __launch_bounds__(kPartialThreads) void router_wgrad_partial_kernel(
+    const float* __restrict__ dw, const float* __restrict__ v, const int32_t* __restrict__ perm, int k,
+    float rs, float* __restrict__ dl, const int32_t* __restrict__ offsets, int E,
     const uint16_t* __restrict__ x_perm, int dim, float* __restrict__ partial) {
+  __shared__ int off_sh[FMOE_MAX_EXPERTS + 1];
+  __shared__ float gsh[kChunkRows];
+  if (threadIdx.x <= E) off_sh[threadIdx.x] = offsets[threadIdx.x];  // one load for all E + 1
+  __syncthreads();
   int c = blockIdx.x, e = 0;
   for (; e < E; ++e) {
-    const int n = expert_chunks(offsets, e);
+    const int n = (off_sh[e + 1] - off_sh[e] + kChunkRows - 1) / kChunkRows;
     if (c < n) break;
     c -= n;
   }
   if (e >= E) return;  // grid is an upper bound on the chunk count
-  const int r0 = offsets[e] + c * kChunkRows;
-  const int r1 = min(offsets[e + 1], r0 + kChunkRows);
+  const int r0 = off_sh[e] + c * kChunkRows;
+  const int r1 = min(off_sh[e + 1], r0 + kChunkRows);
   float* out = partial + static_cast<int64_t>(blockIdx.x) * (dim + 1);
   const int nchunk8 = dim / 8;
-  for (int col8 = threadIdx.x; col8 <= nchunk8; col8 += blockDim.x) {
+  const int64_t ld = dim / 8;
+  // Column passes of kPartialThreads columns (the same count for every
+  // thread, so the barrier in the first pass is reached by all).
+  for (int cb = 0; cb <= nchunk8; cb += kPartialThreads) {
+    const int col8 = cb + threadIdx.x;
+    const bool is_col = col8 < nchunk8;
+    const uint4* xc = reinterpret_cast<const uint4*>(x_perm) + (is_col ? col8 : 0);
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    // Batches of kPartialBatch rows: every load first (rows past r1 read row
+    // r1 - 1, in bounds), then the rows below r1 added in order through a
+    // select, so that no load waits on another.  The first batch's loads go
+    // out before the logit gradients are formed.
+    uint4 xv[kPartialBatch];
+    auto load_batch = [&](int rb) {
+#pragma unroll
+      for (int u = 0; u < kPartialBatch; ++u) xv[u] = xc[static_cast<int64_t>(min(rb + u, r1 - 1)) * ld];
+    };
+    if (is_col) load_batch(r0);
+    if (cb == 0) {
+      if (threadIdx.x < r1 - r0) {
+        const int slot = perm[r0 + threadIdx.x];
+        const int t = slot / k, jr = slot - t * k;
+        const float g = slot_dlogit(dw + static_cast<int64_t>(t) * k, v + static_cast<int64_t>(t) * k, k, jr, rs);
+        dl[slot] = g;
+        gsh[threadIdx.x] = g;
+      }
+      __syncthreads();
+    }
     if (col8 == nchunk8) {  // bias column
-      float acc = 0.0f;
-      for (int r = r0; r < r1; ++r) acc = acc + dl_row[r];
-      out[dim] = acc;
+      float bacc = 0.0f;
+      for (int r = r0; r < r1; ++r) bacc = bacc + gsh[r - r0];
+      out[dim] = bacc;
       continue;
     }
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int rb = r0; rb < r1; rb += 8) {
-      float g[8];
-      uint4 xv[8];
+    if (!is_col) continue;
+    for (int rb = r0; rb < r1; rb += kPartialBatch) {
+      if (rb != r0) load_batch(rb);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int r = min(rb + u, r1 - 1);  // rows past r1 get g = 0
-        g[u] = rb + u < r1 ? dl_row[r] : 0.0f;
-        xv[u] = reinterpret_cast<const uint4*>(x_perm + static_cast<int64_t>(r) * dim)[col8];
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        if (rb + u >= r1) break;
+      for (int u = 0; u < kPartialBatch; ++u) {
+        const bool in = rb + u < r1;
+        const float g = gsh[in ? rb + u - r0 : 0];
         float xf[8];
         unpack8(xv[u], xf);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = fmaf(g[u], xf[i], acc[i]);
+        for (int i = 0; i < 8; ++i) {
+          const float f = fmaf(g, xf[i], acc[i]);
+          acc[i] = in ? f : acc[i];
+        }
       }
     }
 #pragma unroll
@@ -430,12 +538,25 @@ __global__ __launch_bounds__(256) void router_wgrad_final_kernel(
   const int e = blockIdx.y;
   const int cl = threadIdx.x & 15, lanec = threadIdx.x >> 4;
   const int col = blockIdx.x * 16 + cl;
-  int base = 0;
-  for (int q = 0; q < e; ++q) base += expert_chunks(offsets, q);
-  const int nch = expert_chunks(offsets, e);
+  int base = 0;  // uniform: scalar loads of the offsets
+  for (int q = 0; q < e; ++q) base += (offsets[q + 1] - offsets[q] + kChunkRows - 1) / kChunkRows;
+  const int nch = (offsets[e + 1] - offsets[e] + kChunkRows - 1) / kChunkRows;
   float acc = 0.0f;
-  if (col <= dim)
-    for (int c = lanec; c < nch; c += 16) acc = acc + partial[static_cast<int64_t>(base + c) * (dim + 1) + col];
+  if (col <= dim) {
+    const float* pc = partial + static_cast<int64_t>(base) * (dim + 1) + col;
+    int c = lanec;
+    const int last = max(nch - 1, 0);
+    for (; c < nch; c += 16 * 16) {  // sixteen loads in flight (clamped in bounds), added in chunk order
+      float p[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) p[u] = pc[static_cast<int64_t>(min(c + 16 * u, last)) * (dim + 1)];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const float sum = acc + p[u];
+        acc = c + 16 * u < nch ? sum : acc;
+      }
+    }
+  }
   lsum[lanec][cl] = acc;
   __syncthreads();
   if (lanec != 0 || col > dim) return;
@@ -476,7 +597,7 @@ extern "C" int fmoe_router_fwd(const void* x, const void* gate_w, const void* ga
   if (!x || !gate_w || !gate_b || !idx || !weights || !topv) return FMOE_ERR_INVALID_ARG;
   if (!aligned16(x) || !aligned16(gate_w)) return FMOE_ERR_ALIGN;
   const bool small = T <= kRouterSmallT;
-  const int threads = small ? kRouterLanes * (n_experts < 32 ? n_experts : 32) : kRouterTok * kRouterLanes;
+  const int threads = small ? kRouterLanes * (n_experts < 32 ? n_experts : 32) : kRouterThreads;
   const int64_t blocks = small ? T : ceil_div(T, kRouterTok);
   hipStream_t s = as_stream(stream);
   auto xs = static_cast<const uint16_t*>(x);
@@ -489,9 +610,10 @@ extern "C" int fmoe_router_fwd(const void* x, const void* gate_w, const void* ga
                                                                          n_experts, k, route_scale,  \
                                                                          idx, idx64, weights, topv); \
     else                                                                                              \
-      router_fwd_kernel<EB, NQ><<<dim3(blocks), dim3(threads), 0, s>>>(xs, ws, bs, (int)T, (int)dim,  \
+      router_fwd_kernel<EB, NQ, kRouterPerGroup><<<dim3(blocks), dim3(threads), 0, s>>>(xs, ws, bs, (int)T, (int)dim,  \
                                                                        n_experts, k, route_scale,    \
-                                                                       idx, idx64, weights, topv);   \
+                                                                       idx, idx64, weights, topv,    \
+                                                                       nullptr);                     \
   } while (0)
 #define FMOE_ROUTER_LAUNCH_E(NQ)                 \
   do {                                           \
@@ -507,6 +629,37 @@ extern "C" int fmoe_router_fwd(const void* x, const void* gate_w, const void* ga
 #undef FMOE_ROUTER_LAUNCH
   return launch_status();
 }
+
+namespace fmoe {
+// The routing half of fmoe_route_and_dispatch: router_fwd_kernel for any T
+// (for T <= kRouterSmallT it gives the bits of router_small_kernel, which
+// sums each logit in the same order), with each workgroup's per-expert
+// counts written to block_hist[ceil(T / kRouterTok)][E].  Arguments are
+// checked by the caller.
+int launch_router_hist(const uint16_t* xs, const uint16_t* ws, const uint16_t* bs, int64_t T, int64_t dim,
+                       int n_experts, int k, float route_scale, int32_t* idx, int64_t* idx64, float* weights,
+                       float* topv, int32_t* block_hist, hipStream_t s) {
+  const int threads = kRouterThreads;
+  const int64_t blocks = ceil_div(T, kRouterTok);
+#define FMOE_ROUTER_H(EB, NQ)                                                                          \
+  router_fwd_kernel<EB, NQ, kRouterPerGroup><<<dim3(blocks), dim3(threads), 0, s>>>(xs, ws, bs, (int)T, (int)dim, n_experts, \
+                                                                   k, route_scale, idx, idx64, weights,   \
+                                                                   topv, block_hist)
+#define FMOE_ROUTER_H_E(NQ)                              \
+  do {                                                   \
+    if (n_experts <= 8) FMOE_ROUTER_H(8, NQ);            \
+    else if (n_experts <= 16) FMOE_ROUTER_H(16, NQ);     \
+    else if (n_experts <= 32) FMOE_ROUTER_H(32, NQ);     \
+    else FMOE_ROUTER_H(64, NQ);                          \
+  } while (0)
+  if (dim <= 512) FMOE_ROUTER_H_E(4);
+  else if (dim <= 1024) FMOE_ROUTER_H_E(8);
+  else FMOE_ROUTER_H_E(16);
+#undef FMOE_ROUTER_H_E
+#undef FMOE_ROUTER_H
+  return launch_status();
+}
+}  // namespace fmoe
 
 extern "C" int fmoe_route_dispatch(const void* x, const void* gate_w, const void* gate_b, int64_t T,
                                    int64_t dim, int n_experts, int k, float route_scale, int32_t* idx,
@@ -554,8 +707,8 @@ inline int64_t router_max_chunks(int64_t T, int n_experts, int k) {
 
 extern "C" size_t fmoe_router_bwd_workspace_bytes(int64_t T, int64_t dim, int n_experts, int k) {
   if (T <= 0 || dim <= 0 || n_experts <= 0 || k <= 0) return 0;
-  // chunk partials, then the per-row logit gradients
-  return static_cast<size_t>(router_max_chunks(T, n_experts, k) * (dim + 1) + T * k) * sizeof(float);
+  // chunk partials
+  return static_cast<size_t>(router_max_chunks(T, n_experts, k) * (dim + 1)) * sizeof(float);
 }
 
 extern "C" int fmoe_router_bwd(const float* d_weights, const float* topv, const int32_t* perm,
@@ -584,11 +737,9 @@ extern "C" int fmoe_router_bwd(const float* d_weights, const float* topv, const 
   if (!aligned16(x_perm)) return FMOE_ERR_ALIGN;
   const int64_t max_chunks = router_max_chunks(T, n_experts, k);
   float* partial = static_cast<float*>(workspace);
-  float* dl_row = partial + max_chunks * (dim + 1);
-  router_dlogit_kernel<<<dim3(ceil_div(T * k, 256)), dim3(256), 0, s>>>(
-      d_weights, topv, perm, (int)(T * k), k, route_scale, d_logits, dl_row);
   router_wgrad_partial_kernel<<<dim3(max_chunks), dim3(128), 0, s>>>(
-      dl_row, offsets, n_experts, static_cast<const uint16_t*>(x_perm), (int)dim, partial);
+      d_weights, topv, perm, k, route_scale, d_logits, offsets, n_experts,
+      static_cast<const uint16_t*>(x_perm), (int)dim, partial);
   router_wgrad_final_kernel<<<dim3(ceil_div(dim + 1, 16), n_experts), dim3(256), 0, s>>>(
       partial, offsets, n_experts, (int)dim, grad_dtype, d_gate_w, d_gate_b);
   return launch_status();

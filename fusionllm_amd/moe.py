@@ -231,6 +231,9 @@ def _forward_pass(meta, x, gate_w, gate_b, weights, residual=None):
     if 0 < T <= K.TINY_BATCH and T * E <= 64 and d <= 2048:
         # decode-sized: routing and dispatch in one launch (one workgroup)
         idx, idx64, w, v, counts, offsets, perm, pos, x_perm = K.route_dispatch(xb, gwb, gbb, k, rs)
+    elif d <= 2048:
+        # routing with the dispatch histogram, scan, scatter with the row copies: three launches
+        idx, idx64, w, v, counts, offsets, perm, pos, x_perm = K.route_and_dispatch(xb, gwb, gbb, k, rs)
     else:
         idx, idx64, w, v = K.router_fwd(xb, gwb, gbb, k, rs)
         counts, offsets, perm, pos, x_perm = K.dispatch(idx, xb, E)

@@ -102,6 +102,42 @@ def test_dispatch_all_on_one_expert(gpu_device, T):
     assert torch.equal(x_perm.cpu().view(torch.int16), x.view(torch.int16))
 
 
+@pytest.mark.parametrize("T,d,E,k,rs", [(16384, 768, 8, 2, 1.0), (777, 768, 8, 2, 2.5), (1, 768, 8, 2, 1.0),
+                                        (31, 512, 16, 4, 1.0), (32, 768, 8, 2, 1.0), (33, 2048, 64, 6, 1.0),
+                                        (4096, 2048, 64, 6, 1.0), (129, 1024, 32, 8, 1.0), (200, 64, 3, 3, 1.0)])
+def test_route_and_dispatch_equals_router_then_dispatch(gpu_device, T, d, E, k, rs):
+    # fmoe_route_and_dispatch (router with the dispatch histogram, scan, scatter with the row
+    # copies) against fmoe_router_fwd + fmoe_dispatch and the C oracle: every output bit-equal
+    x, gw, gb = _routing_inputs(T, d, E, seed=T + 3 * E)
+    xd, gwd, gbd = x.to(gpu_device), gw.to(gpu_device), gb.to(gpu_device)
+    got = K.route_and_dispatch(xd, gwd, gbd, k, rs)
+    idx, idx64, w, v = K.router_fwd(xd, gwd, gbd, k, rs)
+    ref = (idx, idx64, w, v) + tuple(K.dispatch(idx, xd, E))
+    names = ("idx", "idx64", "weights", "topv", "counts", "offsets", "perm", "pos", "x_perm")
+    for n, a, b in zip(names, got, ref):
+        if a.dtype == torch.float32:
+            a, b = f32_bits(a.cpu()), f32_bits(b.cpu())
+        elif a.dtype == torch.bfloat16:
+            a, b = a.cpu().view(torch.int16), b.cpu().view(torch.int16)
+        assert torch.equal(a.cpu(), b.cpu()), n
+    ridx, _, _ = mo.router_c(x, gw, gb, k, rs)
+    rc, ro, rp, rpos = mo.dispatch_c(ridx, E)
+    assert torch.equal(got[0].cpu(), ridx) and torch.equal(got[6].cpu(), rp) and torch.equal(got[4].cpu(), rc)
+    # without the gather: the same index outputs
+    nog = K.route_and_dispatch(xd, gwd, gbd, k, rs, gather=False)
+    assert nog[8] is None and torch.equal(nog[6].cpu(), rp) and torch.equal(nog[7].cpu(), rpos)
+
+
+def test_route_and_dispatch_empty_batch(gpu_device):
+    d, E, k = 768, 8, 2
+    x = torch.empty(0, d, dtype=torch.bfloat16, device=gpu_device)
+    gw = torch.randn(E, d, device=gpu_device).bfloat16()
+    gb = torch.zeros(E, device=gpu_device).bfloat16()
+    out = K.route_and_dispatch(x, gw, gb, k, 1.0)
+    assert out[4].cpu().tolist() == [0] * E and out[5].cpu().tolist() == [0] * (E + 1)
+    assert out[6].numel() == 0 and out[8].shape == (0, d)
+
+
 # ---- grouped GEMMs -----------------------------------------------------------------
 
 def _groups(counts, dev):

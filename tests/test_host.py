@@ -21,7 +21,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     syms = declared_symbols()
-    assert len(syms) == 25
+    assert len(syms) == 27
     for s in syms:
         assert hasattr(lib, s), s
     assert set(syms) == set(_lib.SIGNATURES), "ctypes binding and header disagree"
@@ -84,10 +84,19 @@ def test_argument_errors_without_gpu():
                                    None, None, None, None) == 2
     assert lib.fmoe_route_dispatch(None, None, None, 4, 768, 8, 2, 1.0, None, None, None, None, None, None,
                                    None, None, None, None) == 1
+    # routing + dispatch of any batch: shape checks before any pointer is used, workspace size
+    assert lib.fmoe_route_and_dispatch(None, None, None, 4, 4096, 8, 2, 1.0, None, None, None, None, None, None,
+                                       None, None, None, None, 0, None) == 2  # dim > 2048
+    assert lib.fmoe_route_and_dispatch(None, None, None, 4, 768, 65, 2, 1.0, None, None, None, None, None, None,
+                                       None, None, None, None, 0, None) == 7
+    assert lib.fmoe_route_and_dispatch(None, None, None, 4, 768, 8, 2, 1.0, None, None, None, None, None, None,
+                                       None, None, None, None, 0, None) == 1  # null outputs
+    assert lib.fmoe_route_and_dispatch_workspace_bytes(16384, 8, 2) == 2 * 512 * 8 * 4
+    assert lib.fmoe_route_and_dispatch_workspace_bytes(33, 64, 6) == 2 * 2 * 64 * 4
     # size queries
     assert lib.fmoe_dispatch_workspace_bytes(16384, 8, 2) == 2 * 128 * 8 * 4
     assert lib.fmoe_weight_grad_workspace_bytes(32768, 16384, 8, 768, 2048) > 0
-    assert lib.fmoe_router_bwd_workspace_bytes(16384, 768, 8, 2) == ((16384 * 2 // 32 + 8) * 769 + 16384 * 2) * 4
+    assert lib.fmoe_router_bwd_workspace_bytes(16384, 768, 8, 2) == (16384 * 2 // 32 + 8) * 769 * 4
     assert lib.fmoe_norm_bwd_workspace_bytes(768) == 4160 * 768 * 4
     # fused NorMuon step: limits checked before any pointer is used
     import ctypes
