@@ -47,19 +47,20 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_hist_kernel(
     block_hist[static_cast<int64_t>(blockIdx.x) * E + e] = cnt[e];
 }
 
-// One workgroup of 16 waves; wave w scans experts w, w + 16, ...
-// block_base[b][e] = offsets[e] + sum_{b' < b} block_hist[b'][e]: pass 1 adds
-// each expert's block counts (wave reduction), thread 0 turns the totals into
-// offsets, pass 2 writes the per-block bases with a 64-lane inclusive scan
-// (shfl_up) per chunk of 64 blocks, carried across chunks.  When the block
-// counts fit (nblocks * E <= kScanStaged) they are first copied to LDS with
-// every thread's loads in flight at once; with at most 16 experts and 1024
-// blocks the two passes then become one (a lane per run of blocks, one
-// 64-lane scan per expert).  Integer sums, so the order does not change the
-// result.
+// One workgroup of 16 waves.  block_base[b][e] = offsets[e] + sum_{b' < b}
+// block_hist[b'][e].  Wave-row path (E divides 64): lane l takes expert
+// l % E of the block rows l / E, l / E + 64 / E, ... of a contiguous range of
+// blocks per wave, consecutive lanes reading consecutive counts, kScanBatch
+// loads in flight at a time; the waves' per-expert sums meet in LDS, wave 0
+// forms the totals and offsets (one 64-lane scan), and each wave then reads
+// its blocks again (from L2) and walks them in order with shuffles across the
+// lanes of an expert.  Otherwise: pass 1 adds each expert's block counts
+// (wave reduction), pass 2 writes the per-block bases with a 64-lane
+// inclusive scan (shfl_up) per chunk of 64 blocks, carried across chunks.
+// Integer sums, so the order does not change the result.
 constexpr int kScanThreads = 1024;
-constexpr int kScanStaged = 12288;  // 48 KB of LDS
-constexpr int kScanRun = 16;        // one-pass path: up to 64 * 16 blocks, one expert per wave
+constexpr int kScanWaves = kScanThreads / 64;
+constexpr int kScanBatch = 16;  // loads per lane in flight on the wave-row path
 
 __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 #pragma unroll
@@ -75,74 +76,75 @@ __global__ __launch_bounds__(kScanThreads) void dispatch_scan_kernel(
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets) {
   __shared__ int total[FMOE_MAX_EXPERTS];
   __shared__ int start[FMOE_MAX_EXPERTS + 1];
-  __shared__ int hsh[kScanStaged];
+  __shared__ int wsum[kScanWaves][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  constexpr int nwaves = kScanThreads / 64;
-  const int n = nblocks * E;
-  const bool staged = n <= kScanStaged;  // uniform over the workgroup
-  if (staged) {
-    int hv[kScanStaged / kScanThreads];  // every load issued before the first LDS store
-#pragma unroll
-    for (int u = 0; u < kScanStaged / kScanThreads; ++u) {
-      const int i = threadIdx.x + u * kScanThreads;
-      hv[u] = i < n ? block_hist[i] : 0;
-    }
-#pragma unroll
-    for (int u = 0; u < kScanStaged / kScanThreads; ++u) {
-      const int i = threadIdx.x + u * kScanThreads;
-      if (i < n) hsh[i] = hv[u];
-    }
-    __syncthreads();
-  }
-  const int* src = staged ? hsh : block_hist;
-  if (staged && E <= nwaves && nblocks <= 64 * kScanRun) {
-    // One pass: wave e takes expert e; lane l owns the run of blocks
-    // [l * run, (l + 1) * run), kept in registers.  A 64-lane scan of the run
-    // sums gives each run's first base and the expert's total.
-    const int run = (nblocks + 63) / 64;
-    const int e = wave;
-    int hv[kScanRun];
+  const int per = (E > 0 && 64 % E == 0) ? 64 / E : 0;  // block rows per load instruction
+  if (per) {  // uniform over the workgroup
+    const int bw = ((nblocks + kScanWaves - 1) / kScanWaves + per - 1) / per * per;  // blocks per wave
+    const int its = bw / per;
+    const int e = lane % E, sub = lane / E;
+    const int b0 = wave * bw;
     int loc = 0;
+    for (int i0 = 0; i0 < its; i0 += kScanBatch) {
+      int hv[kScanBatch];
 #pragma unroll
-    for (int j = 0; j < kScanRun; ++j) {
-      const int b = lane * run + j;
-      hv[j] = (e < E && j < run && b < nblocks) ? hsh[b * E + e] : 0;
-      loc += hv[j];
-    }
-    const int incl = wave_incl_scan(loc, lane);
-    if (e < E && lane == 63) total[e] = incl;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      int acc = 0;
-      for (int q = 0; q < E; ++q) { start[q] = acc; acc += total[q]; }
-      start[E] = acc;
-    }
-    __syncthreads();
-    for (int q = threadIdx.x; q < E; q += kScanThreads) {
-      counts[q] = total[q];
-      offsets[q] = start[q];
-    }
-    if (threadIdx.x == 0) offsets[E] = start[E];
-    // bases to LDS (over the staged counts, all read by now), then copied out coalesced
-    __syncthreads();
-    if (e < E) {
-      int base = start[e] + incl - loc;
+      for (int u = 0; u < kScanBatch; ++u) {
+        const int b = b0 + (i0 + u) * per + sub;
+        hv[u] = (i0 + u < its && b < nblocks) ? block_hist[static_cast<int64_t>(b) * E + e] : 0;
+      }
 #pragma unroll
-      for (int j = 0; j < kScanRun; ++j) {
-        const int b = lane * run + j;
-        if (j < run && b < nblocks) {
-          hsh[b * E + e] = base;
-          base += hv[j];
-        }
+      for (int u = 0; u < kScanBatch; ++u) loc += hv[u];
+    }
+    int tot = loc;  // over the lanes of expert e: xor offsets E, 2E, ..., 32
+    for (int off = E; off < 64; off <<= 1) tot += __shfl_xor(tot, off, 64);
+    if (sub == 0) wsum[wave][e] = tot;
+    __syncthreads();
+    if (wave == 0) {
+      int t = 0;
+      if (lane < E)
+        for (int w = 0; w < kScanWaves; ++w) t += wsum[w][lane];
+      const int incl = wave_incl_scan(t, lane);
+      if (lane < E) {
+        total[lane] = t;
+        start[lane] = incl - t;
+        counts[lane] = t;
+        offsets[lane] = incl - t;
+      }
+      if (lane == 63) {
+        start[E] = incl;
+        offsets[E] = incl;
       }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += kScanThreads) block_base[i] = hsh[i];
+    int base = start[e];
+    for (int w = 0; w < wave; ++w) base += wsum[w][e];
+    for (int i0 = 0; i0 < its; i0 += kScanBatch) {
+      int hv[kScanBatch];
+#pragma unroll
+      for (int u = 0; u < kScanBatch; ++u) {
+        const int b = b0 + (i0 + u) * per + sub;
+        hv[u] = (i0 + u < its && b < nblocks) ? block_hist[static_cast<int64_t>(b) * E + e] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < kScanBatch; ++u) {
+        if (i0 + u < its) {  // uniform
+          int incl = hv[u];  // inclusive over sub (lanes e, e + E, ...)
+          for (int off = 1; off < per; off <<= 1) {
+            const int v = __shfl_up(incl, off * E, 64);
+            if (sub >= off) incl += v;
+          }
+          const int b = b0 + (i0 + u) * per + sub;
+          if (b < nblocks) block_base[static_cast<int64_t>(b) * E + e] = base + incl - hv[u];
+          base += __shfl(incl, (per - 1) * E + e, 64);  // the row's count for expert e
+        }
+      }
+    }
     return;
   }
+  constexpr int nwaves = kScanWaves;
   for (int e = wave; e < E; e += nwaves) {
     int sum = 0;
-    for (int b = lane; b < nblocks; b += 64) sum += src[static_cast<int64_t>(b) * E + e];
+    for (int b = lane; b < nblocks; b += 64) sum += block_hist[static_cast<int64_t>(b) * E + e];
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
     if (lane == 0) total[e] = sum;
@@ -164,7 +166,7 @@ __global__ __launch_bounds__(kScanThreads) void dispatch_scan_kernel(
     for (int b0 = 0; b0 < nblocks; b0 += 64) {
       const int b = b0 + lane;
       const int64_t o = static_cast<int64_t>(b) * E + e;
-      const int h = b < nblocks ? src[o] : 0;
+      const int h = b < nblocks ? block_hist[o] : 0;
       const int incl = wave_incl_scan(h, lane);
       if (b < nblocks) block_base[o] = carry + incl - h;
       carry += __shfl(incl, 63, 64);

@@ -104,7 +104,10 @@ def test_dispatch_all_on_one_expert(gpu_device, T):
 
 @pytest.mark.parametrize("T,d,E,k,rs", [(16384, 768, 8, 2, 1.0), (777, 768, 8, 2, 2.5), (1, 768, 8, 2, 1.0),
                                         (31, 512, 16, 4, 1.0), (32, 768, 8, 2, 1.0), (33, 2048, 64, 6, 1.0),
-                                        (4096, 2048, 64, 6, 1.0), (129, 1024, 32, 8, 1.0), (200, 64, 3, 3, 1.0)])
+                                        (4096, 2048, 64, 6, 1.0), (129, 1024, 32, 8, 1.0), (200, 64, 3, 3, 1.0),
+                                        # many scan blocks: 2048 (and 1024 in fmoe_dispatch) with 64 experts;
+                                        # 1250 (313) with 5 experts, which do not divide 64
+                                        (65536, 256, 64, 4, 1.0), (40000, 128, 5, 2, 1.0)])
 def test_route_and_dispatch_equals_router_then_dispatch(gpu_device, T, d, E, k, rs):
     # fmoe_route_and_dispatch (router with the dispatch histogram, scan, scatter with the row
     # copies) against fmoe_router_fwd + fmoe_dispatch and the C oracle: every output bit-equal
