@@ -588,6 +588,23 @@ def main():
         dom = max(kernels, key=lambda n: kernels[n]["share"])
         timer = {}
     dk = (table_of(timer, args.steps, elapsed) if timer else kernels)[dom]
+    if not args.graph and not args.fwd_only:
+        # GEMM pass: as many steps as the table pass, with HIP events around
+        # the grouped GEMMs only (each 150 us or longer at C2, so the gaps the
+        # events leave are small beside them).  The GEMM rows of the table and
+        # the grouped-GEMM fraction come from it: the table pass brackets every
+        # entry point, and its gaps between the short kernels (the GPU idles,
+        # clocks drop) make the GEMMs measure 10-15 % slower than in a step.
+        gtimer = {}
+        K.set_timer(gtimer, only={n for n, (b, _) in model.items() if b == "mfma"})
+        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        g0.record()
+        for _ in range(table_steps):
+            step()
+        g1.record()
+        torch.cuda.synchronize()
+        K.set_timer(None)
+        kernels.update(table_of(gtimer, table_steps, g0.elapsed_time(g1) / 1e3))
     if not args.fwd_only and not norms and not args.autocast:
         # the HBM-bound entry points from graphs of back-to-back launches
         step_us = elapsed / args.steps * 1e6
