@@ -131,6 +131,40 @@ def test_route_and_dispatch_equals_router_then_dispatch(gpu_device, T, d, E, k, 
     assert nog[8] is None and torch.equal(nog[6].cpu(), rp) and torch.equal(nog[7].cpu(), rpos)
 
 
+@pytest.mark.parametrize("case", ["all_tied", "one_expert"])
+def test_route_and_dispatch_degenerate_routing(gpu_device, case):
+    # all_tied: zero gate and bias, so every score is 0.5 and each token takes experts 0..k-1
+    # (lowest index first), two full groups and six empty ones; one_expert: a bias that puts
+    # every first choice on expert 5.  Against router + dispatch and the C oracle.
+    T, d, E, k = 5000, 768, 8, 2
+    x, gw, gb = _routing_inputs(T, d, E, seed=11)
+    if case == "all_tied":
+        gw = torch.zeros_like(gw)
+        gb = torch.zeros_like(gb)
+    else:
+        gb = torch.full_like(gb, -20.0)
+        gb[5] = 20.0
+    xd, gwd, gbd = x.to(gpu_device), gw.to(gpu_device), gb.to(gpu_device)
+    got = K.route_and_dispatch(xd, gwd, gbd, k, 1.0)
+    idx, idx64, w, v = K.router_fwd(xd, gwd, gbd, k, 1.0)
+    ref = (idx, idx64, w, v) + tuple(K.dispatch(idx, xd, E))
+    for a, b in zip(got, ref):
+        if a.dtype == torch.float32:
+            a, b = f32_bits(a.cpu()), f32_bits(b.cpu())
+        elif a.dtype == torch.bfloat16:
+            a, b = a.cpu().view(torch.int16), b.cpu().view(torch.int16)
+        assert torch.equal(a.cpu(), b.cpu())
+    ridx, _, _ = mo.router_c(x, gw, gb, k, 1.0)
+    rc, ro, rp, rpos = mo.dispatch_c(ridx, E)
+    assert torch.equal(got[0].cpu(), ridx) and torch.equal(got[6].cpu(), rp)
+    counts = got[4].cpu().tolist()
+    if case == "all_tied":
+        assert counts == [T, T] + [0] * (E - 2)
+        assert torch.equal(got[0].cpu(), torch.tensor([[0, 1]] * T, dtype=torch.int32))
+    else:
+        assert counts[5] == T and sum(counts) == T * k
+
+
 def test_route_and_dispatch_empty_batch(gpu_device):
     d, E, k = 768, 8, 2
     x = torch.empty(0, d, dtype=torch.bfloat16, device=gpu_device)
