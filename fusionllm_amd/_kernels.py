@@ -93,6 +93,7 @@ def router_fwd(x, gate_w, gate_b, k: int, route_scale: float):
 
 
 TINY_BATCH = 16  # fmoe_route_dispatch takes up to this many tokens
+ROUTER_SMALL_T = 128  # fmoe_router_fwd runs one workgroup per token up to this many tokens
 
 
 @_timed

@@ -231,8 +231,10 @@ def _forward_pass(meta, x, gate_w, gate_b, weights, residual=None):
     if 0 < T <= K.TINY_BATCH and T * E <= 64 and d <= 2048:
         # decode-sized: routing and dispatch in one launch (one workgroup)
         idx, idx64, w, v, counts, offsets, perm, pos, x_perm = K.route_dispatch(xb, gwb, gbb, k, rs)
-    elif d <= 2048:
-        # routing with the dispatch histogram, scan, scatter with the row copies: three launches
+    elif d <= 2048 and T > K.ROUTER_SMALL_T:
+        # routing with the dispatch histogram, scan, scatter with the row copies: three launches.
+        # Up to ROUTER_SMALL_T tokens the router's one-workgroup-per-token kernel and the
+        # one-launch small dispatch below are faster (C3 replay at 32 tokens: 49 against 55 us).
         idx, idx64, w, v, counts, offsets, perm, pos, x_perm = K.route_and_dispatch(xb, gwb, gbb, k, rs)
     else:
         idx, idx64, w, v = K.router_fwd(xb, gwb, gbb, k, rs)
