@@ -138,7 +138,9 @@ int fmoe_route_dispatch(const void* x, const void* gate_w, const void* gate_b,
  * scatter copies each block's rows into x_perm itself.  The outputs are those
  * of fmoe_router_fwd followed by fmoe_dispatch on its idx, bit for bit.
  * dim <= 2048; x_perm may be NULL (no gather); workspace: see the query
- * (2 * ceil(T / 32) * E int32). */
+ * (2 * ceil(T / 32) * E int32).  Meant for more than 128 tokens: up to 128,
+ * fmoe_router_fwd (one workgroup per token) and fmoe_dispatch (one launch up
+ * to 256 slots) are faster. */
 size_t fmoe_route_and_dispatch_workspace_bytes(int64_t T, int n_experts, int k);
 int fmoe_route_and_dispatch(const void* x, const void* gate_w, const void* gate_b,
                             int64_t T, int64_t dim, int n_experts, int k, float route_scale,
