@@ -15,6 +15,8 @@ Every function follows the reference op by op, in the reference's dtypes:
   gate_bias_step  moe.py:89-98   bincount, 1.10/0.90 x mean thresholds, masked +-speed
   load_balance_loss moe.py:100-109 E * sum(f * P) with one-hot P
   normuon_step    training/optimizer.py:18-58 NorMuon.step on one parameter
+  router_dlogits  autograd of moe.py:46-49 for the selected scores, fp32 numpy
+                  in the order the router backward kernel computes it
 Router modes:
   "module" — the reference exactly: logits and scores in the module dtype,
              torch.topk (its own tie order);
@@ -279,6 +281,36 @@ def dispatch_c(idx: torch.Tensor, n_experts: int):
     if lib.oracle_dispatch(P(a), T, n_experts, k, P(counts), P(offsets), P(perm), P(pos)) != 0:
         raise ValueError("expert index out of range")
     return tuple(torch.from_numpy(z) for z in (counts, offsets, perm, pos))
+
+
+def router_dlogits(d_w: np.ndarray, topv: np.ndarray, route_scale: float) -> np.ndarray:
+    """dL/dlogit for each selected expert, fp32 [T, k]: the autograd of
+    w = v / (sum_j v_j + 1e-10) * route_scale (moe.py:49) followed by the
+    top-k scatter (moe.py:48) and the sigmoid backward (moe.py:47) of the
+    selected logits, per token with the sums over j in ascending order:
+      D = (v_0 + v_1 + ...) + 1e-10,   dq_j = dw_j * rs,
+      dS = 0 - (dq_0 v_0)/(D D) - (dq_1 v_1)/(D D) - ...,
+      dv_j = dq_j / D + dS,   dlogit_j = (dv_j * (1 - v_j)) * v_j.
+    Every operation is a single IEEE fp32 operation (no fused multiply-add)."""
+    dw = np.asarray(d_w, np.float32)
+    v = np.asarray(topv, np.float32)
+    k = v.shape[1]
+    rs = np.float32(route_scale)
+    s = v[:, 0].copy()
+    for j in range(1, k):
+        s = (s + v[:, j]).astype(np.float32)
+    D = (s + np.float32(1e-10)).astype(np.float32)
+    DD = (D * D).astype(np.float32)
+    dS = np.zeros_like(D)
+    for j in range(k):
+        dq = (dw[:, j] * rs).astype(np.float32)
+        dS = (dS - ((dq * v[:, j]).astype(np.float32) / DD).astype(np.float32)).astype(np.float32)
+    out = np.empty_like(v)
+    for j in range(k):
+        dq = (dw[:, j] * rs).astype(np.float32)
+        dv = ((dq / D).astype(np.float32) + dS).astype(np.float32)
+        out[:, j] = ((dv * (np.float32(1.0) - v[:, j]).astype(np.float32)).astype(np.float32) * v[:, j]).astype(np.float32)
+    return out
 
 
 def expf_c(x: float) -> float:

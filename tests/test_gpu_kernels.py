@@ -175,6 +175,46 @@ def test_route_and_dispatch_empty_batch(gpu_device):
     assert out[6].numel() == 0 and out[8].shape == (0, d)
 
 
+@pytest.mark.parametrize("T,d,E,k,gdt,empty", [(16384, 768, 8, 2, torch.bfloat16, None),
+                                              (777, 512, 8, 2, torch.float32, 3),
+                                              (2000, 2048, 64, 6, torch.bfloat16, None),
+                                              (129, 256, 6, 3, torch.float32, None),
+                                              (1, 64, 4, 2, torch.float32, None)])
+def test_router_bwd(gpu_device, T, d, E, k, gdt, empty):
+    # fmoe_router_bwd (logit gradients formed inside the gate partial kernel, chunk partials
+    # added in chunk order): d_logits bit-equal to the oracle's fp32 restatement of the
+    # autograd of moe.py:46-49; the gate weight and bias gradients against their fp64
+    # closed forms sum_{slots of e} dlogit * x_token and sum_{slots of e} dlogit, an expert
+    # without slots exactly zero.  Shapes cover chunk tails (experts of non-multiples of 32
+    # rows), 64 experts at top-6 and a single token.
+    rs = 1.5
+    x, gw, gb = _routing_inputs(T, d, E, seed=T + E)
+    if empty is not None:
+        gb = gb.clone()
+        gb[empty] = -30.0  # never selected
+    xd, gwd, gbd = x.to(gpu_device), gw.to(gpu_device), gb.to(gpu_device)
+    idx, _, _, v = K.router_fwd(xd, gwd, gbd, k, rs)
+    counts, offsets, perm, pos, x_perm = K.dispatch(idx, xd, E)
+    g = torch.Generator().manual_seed(5)
+    d_w = torch.randn(T, k, generator=g).float()
+    d_logits, dgw, dgb = K.router_bwd(d_w.to(gpu_device), v, perm, offsets, x_perm, E, rs, gdt)
+    ref_dl = mo.router_dlogits(d_w.numpy(), v.cpu().numpy(), rs)
+    assert torch.equal(f32_bits(d_logits.cpu()), f32_bits(torch.from_numpy(ref_dl)))
+    dl64 = torch.from_numpy(ref_dl).double().reshape(-1)
+    e_of = idx.cpu().long().reshape(-1)
+    tok = torch.arange(T).repeat_interleave(k)
+    W = torch.zeros(E, d, dtype=torch.float64).index_add_(0, e_of, dl64[:, None] * x.double()[tok])
+    B = torch.zeros(E, dtype=torch.float64).index_add_(0, e_of, dl64)
+    tol = 2e-5 if gdt == torch.float32 else 4e-3
+    for got, ref in ((dgw.cpu().double(), W), (dgb.cpu().double(), B)):
+        assert got.dtype == torch.float64 and torch.isfinite(got).all()
+        err = (got - ref).norm() / max(ref.norm().item(), 1e-30)
+        assert err <= tol, err
+    if empty is not None:
+        assert counts.cpu()[empty].item() == 0
+        assert not dgw.cpu()[empty].any() and dgb.cpu()[empty].item() == 0
+
+
 # ---- grouped GEMMs -----------------------------------------------------------------
 
 def _groups(counts, dev):

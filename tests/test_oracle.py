@@ -188,6 +188,31 @@ def test_planted_router_mistake_is_caught():
     assert not torch.allclose(logits.double(), dropped_bias, atol=1e-6)
 
 
+@pytest.mark.parametrize("k,rs", [(1, 1.0), (2, 1.0), (6, 2.5), (8, 1.0)])
+def test_router_dlogits_against_fp64_autograd(k, rs):
+    # The fp32 restatement of the router backward against torch's fp64 autograd of the
+    # reference's normalisation (moe.py:49) and sigmoid (moe.py:47) on the same scores:
+    # w = v / (sum v + 1e-10) * rs, dlogit = dv * v * (1 - v).
+    g = torch.Generator().manual_seed(7 + k)
+    T = 4096
+    v = torch.rand(T, k, generator=g, dtype=torch.float64) * 0.98 + 0.01
+    v = v.float()
+    d_w = torch.randn(T, k, generator=g).float()
+    got = mo.router_dlogits(d_w.numpy(), v.numpy(), rs)
+    v64 = v.double().requires_grad_(True)
+    w = v64 / (v64.sum(-1, keepdim=True) + 1e-10) * rs
+    w.backward(d_w.double())
+    ref = v64.grad * v64.detach() * (1 - v64.detach())
+    err = np.abs(got.astype(np.float64) - ref.numpy())
+    scale = np.abs(d_w.numpy()).max() * rs
+    assert err.max() <= 1e-5 * scale, err.max()
+    if k >= 2:  # (k = 1: w = v / (v + 1e-10) is flat, the gradient is ~0)
+        # planted mistakes the bound catches: a dropped normalisation term, a sign flip
+        dropped = v64.detach() * (1 - v64.detach()) * d_w.double() * rs / v64.detach().sum(-1, keepdim=True)
+        assert np.abs(dropped.numpy() - ref.numpy()).max() > 1e-3 * scale
+        assert np.abs(-got - ref.numpy()).max() > 1e-3 * scale
+
+
 # ---- dispatch -------------------------------------------------------------------
 
 @pytest.mark.parametrize("T,E,k", [(1, 8, 2), (37, 8, 2), (4096, 8, 2), (1000, 64, 6)])
