@@ -215,6 +215,86 @@ def test_router_bwd(gpu_device, T, d, E, k, gdt, empty):
         assert not dgw.cpu()[empty].any() and dgb.cpu()[empty].item() == 0
 
 
+def _combine_inputs(T, d, E, k, dev, seed):
+    x, gw, gb = _routing_inputs(T, d, E, seed=seed)
+    idx, _, w, _ = K.router_fwd(x.to(dev), gw.to(dev), gb.to(dev), k, 1.0)
+    counts, offsets, perm, pos, _ = K.dispatch(idx, x.to(dev), E, gather=False)
+    g = torch.Generator().manual_seed(seed + 1)
+    o = torch.randn(T * k + T, d, generator=g).bfloat16()  # routed rows, then the shared rows
+    return x, gw, idx, w, perm, pos, o
+
+
+@pytest.mark.parametrize("T,d,E,k", [(4096, 768, 8, 2), (333, 512, 64, 6), (1, 64, 4, 2)])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shared", [True, False])
+def test_combine_fwd_is_index_add_in_expert_order(gpu_device, T, d, E, k, out_dtype, shared):
+    # fmoe_combine_fwd against torch's own ops in the reference's order (moe.py:65-77,87):
+    # y = zeros fp32; per expert ascending, y[tok] += (out * w).to(fp32); y.to(x.dtype); + shared.
+    # Bit-exact: every product and add is one IEEE fp32 operation in that order.
+    x, gw, idx, w, perm, pos, o = _combine_inputs(T, d, E, k, gpu_device, seed=17 + T)
+    rows_r = T * k
+    y = K.combine_fwd(o.to(gpu_device), idx, w, pos, rows_r, shared, out_dtype, None)
+    idx_c, w_c, pos_c = idx.cpu().long(), w.cpu(), pos.cpu().long().reshape(T, k)
+    order = torch.argsort(idx_c, dim=1, stable=True)  # a token's choices by ascending expert
+    acc = torch.zeros(T, d, dtype=torch.float32)
+    for jj in range(k):
+        sel = order[:, jj:jj + 1]
+        rows = pos_c.gather(1, sel)[:, 0]
+        acc = acc + o.float()[rows] * w_c.gather(1, sel)
+    ref = acc.to(out_dtype)
+    if shared:
+        ref = ref + o[rows_r:].to(out_dtype)
+    got = y.cpu()
+    if out_dtype == torch.bfloat16:
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    else:
+        assert torch.equal(f32_bits(got), f32_bits(ref))
+
+
+@pytest.mark.parametrize("T,d,E,k", [(4096, 768, 8, 2), (333, 512, 64, 6)])
+def test_combine_bwd(gpu_device, T, d, E, k):
+    # d_o[r] = bf16(dy[t] * w_slot) bit-exact (moe.py:76 backward of out * w); d_w[slot] =
+    # <dy[t], o[r]> against its fp64 closed form.
+    x, gw, idx, w, perm, pos, o = _combine_inputs(T, d, E, k, gpu_device, seed=31 + T)
+    g = torch.Generator().manual_seed(3)
+    dy = torch.randn(T, d, generator=g).bfloat16()
+    rows_r = T * k
+    o_r = o[:rows_r]
+    d_o, d_w = K.combine_bwd(dy.to(gpu_device), o_r.to(gpu_device), w, perm, k)
+    perm_c = perm.cpu().long()
+    tok, slot = perm_c // k, perm_c
+    ref_do = (dy.float()[tok] * w.cpu().reshape(-1)[slot][:, None]).bfloat16()
+    assert torch.equal(d_o.cpu().view(torch.int16), ref_do.view(torch.int16))
+    ref_dw = torch.zeros(T * k, dtype=torch.float64)
+    ref_dw[slot] = (dy.double()[tok] * o_r.double()).sum(1)
+    got = d_w.cpu().reshape(-1).double()
+    l1 = torch.zeros(T * k, dtype=torch.float64)
+    l1[slot] = (dy.double()[tok] * o_r.double()).abs().sum(1)  # fp32 sum of d terms: error <= ~d ulps of this
+    assert ((got - ref_dw).abs() <= 2e-5 * l1).all()
+
+
+@pytest.mark.parametrize("T,d,E,k", [(4096, 768, 8, 2), (333, 512, 64, 6)])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_dx_reduce(gpu_device, T, d, E, k, out_dtype):
+    # dx[t] = sum of the token's routed rows (ascending expert) + its shared row + the router
+    # term sum_j dlogit_j * Wg[e_j] (the gate Linear's input gradient), against fp64.
+    x, gw, idx, w, perm, pos, o = _combine_inputs(T, d, E, k, gpu_device, seed=47 + T)
+    g = torch.Generator().manual_seed(9)
+    dl = torch.randn(T, k, generator=g).float() * 0.1
+    rows_r = T * k
+    dx = K.dx_reduce(o.to(gpu_device), pos, idx, dl.to(gpu_device), gw.to(gpu_device), rows_r, True, out_dtype)
+    pos_c, idx_c = pos.cpu().long().reshape(T, k), idx.cpu().long()
+    ref = o.double()[rows_r:].clone()
+    l1 = ref.abs()  # sum of the terms' magnitudes: the fp32 sums' error scales with it
+    for j in range(k):
+        a, b = o.double()[pos_c[:, j]], dl.double()[:, j:j + 1] * gw.double()[idx_c[:, j]]
+        ref += a + b
+        l1 += a.abs() + b.abs()
+    got = dx.cpu().double()
+    bound = 1e-6 * l1 + (2.0 ** -8 * ref.abs() if out_dtype == torch.bfloat16 else 0.0)
+    assert ((got - ref).abs() <= bound).all()
+
+
 # ---- grouped GEMMs -----------------------------------------------------------------
 
 def _groups(counts, dev):
