@@ -191,17 +191,18 @@ def gateup_fwd(x_perm, x_shared, offsets, n_experts: int, w1s, w3s, inter: int):
     rows = rows_r + rows_s
     ab = torch.empty(rows, 2 * inter, dtype=torch.bfloat16, device=dev)
     h = torch.empty(rows, inter, dtype=torch.bfloat16, device=dev)
+    ws, ws_bytes = _split_workspace(dev)
     check(lib.fmoe_gateup_fwd(_req(x_perm, "x_perm", torch.bfloat16),
                               _req(x_shared, "x", torch.bfloat16) if x_shared is not None else None,
                               _req(offsets, "offsets", torch.int32), n_experts, rows_r, rows_s, d, inter,
                               ptr_array([w.data_ptr() for w in w1s]), ptr_array([w.data_ptr() for w in w3s]),
-                              ab.data_ptr(), h.data_ptr(), _stream()),
+                              ab.data_ptr(), h.data_ptr(), ws.data_ptr(), ws_bytes, _stream()),
           "fmoe_gateup_fwd")
     return ab, h
 
 
 def _split_workspace(dev):
-    """fp32 workspace for the K-split last round of the plain-output products."""
+    """fp32 workspace for the K-split last round of the row products."""
     lib = _lib.load()
     nbytes = lib.fmoe_split_workspace_bytes()
     return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev), nbytes
@@ -279,11 +280,12 @@ def down_bwd_dx(d_out_routed, d_out_shared, offsets, n_experts: int, w2t, ab, in
     if tuple(w2t.shape) != (G, inter, d):
         raise RuntimeError(f"w2t must be {(G, inter, d)} (got {tuple(w2t.shape)})")
     d_ab = torch.empty(rows_r + rows_s, 2 * inter, dtype=torch.bfloat16, device=ab.device)
+    ws, ws_bytes = _split_workspace(ab.device)
     check(lib.fmoe_down_bwd_dx(_req(d_out_routed, "d_out", torch.bfloat16),
                                _req(d_out_shared, "d_out_shared", torch.bfloat16) if d_out_shared is not None else None,
                                _req(offsets, "offsets", torch.int32), n_experts, rows_r, rows_s, d, inter,
                                _req(w2t, "w2t", torch.bfloat16), _req(ab, "ab", torch.bfloat16),
-                               d_ab.data_ptr(), _stream()),
+                               d_ab.data_ptr(), ws.data_ptr(), ws_bytes, _stream()),
           "fmoe_down_bwd_dx")
     return d_ab
 

@@ -63,7 +63,7 @@ struct GemmArgs {
   const uint16_t* b1[FMOE_MAX_EXPERTS + 1];  // w3 (GATEUP_FWD only)
   int small_max;  // groups with 1 .. small_max rows go to small_gemm_kernel (0: none)
   int small_compact;  // DOWN_FWD small kernel: the grid covers only groups with rows
-  float* split_ws;  // DOWN_FWD / GATEUP_BWD: fp32 partials of K-split tiles (nullptr: no split)
+  float* split_ws;  // fp32 partials of the K-split tiles of the last round (nullptr: no split)
 };
 
 // ---- tiled row-grouped kernel ----------------------------------------------
@@ -126,30 +126,41 @@ constexpr int epi_stores() {
   return MODE == GATEUP_FWD ? 24 : (MODE == DOWN_BWD ? 32 : 16);
 }
 
-// K-split of the last, partial round of tiles (plain-output products only).
-// With T tiles on P workgroups, the T mod P tiles of the last round would run
-// on a fraction of the CUs; instead each is split into S K ranges (S <= 4,
-// R * S <= P, at least 4 K steps per range) whose fp32 partials
-// split_reduce_kernel adds in range order.  Work items: tiles 0 .. full-1 whole,
-// then R * S ranges.
+// K-split of the last, partial round of tiles.  With T tiles on P
+// workgroups, the T mod P tiles of the last round would run on a fraction of
+// the CUs; instead each is split into S K ranges (S <= 4, R * S <= P, at
+// least 4 K steps per range) whose fp32 partials a split reduction adds in
+// range order before the product's epilogue.  Work items: tiles 0 .. full-1
+// whole, then R * S ranges.
+// Only for runs of fewer than kSplitMaxRounds full rounds.  Measured on
+// MI355X (split minus whole, same process): at T=16384, d=768, I=2048 the
+// split gains 12 us on the down product (2 rounds, 32 K steps), 47 us on the
+// gate/up backward (2 rounds, 64 K steps) and 3 us on the down backward (6
+// rounds, 12 K steps) but loses 9 us on the gate/up forward (12 rounds, 12
+// K steps); at d=2048, I=1408, 64 experts (21 to 38 rounds) it loses 1 to
+// 15 us on every product.  Over many rounds the workgroups' finishing times
+// spread by about a tile anyway, and the partials' HBM traffic (written and
+// read once, 256 KB per range) is then not repaid.
 struct SplitPlan {
   int full, R, S;
   __device__ __forceinline__ int items() const { return full + R * S; }
 };
+constexpr int kSplitMaxS = 4;       // K ranges per split tile
+constexpr int kSplitMaxRounds = 8;  // full rounds above which no tile is split
+constexpr int kReduceParts = 16;  // blocks of a split reduction per split tile, 16 rows each
+
 template <int MODE>
 __device__ __forceinline__ SplitPlan split_plan(const GemmArgs& a, int T, int P, int nk) {
   SplitPlan sp{T, 0, 1};
-  if constexpr (MODE == DOWN_FWD || MODE == GATEUP_BWD) {
-    if (a.split_ws == nullptr || T <= 0) return sp;
-    const int R = T % P;
-    if (R == 0) return sp;
-    int S = min(P / R, 4);
-    S = min(S, nk / 4);
-    if (S < 2) return sp;
-    sp.full = T - R;
-    sp.R = R;
-    sp.S = S;
-  }
+  if (a.split_ws == nullptr || T <= 0) return sp;
+  const int R = T % P;
+  if (R == 0 || T / P >= kSplitMaxRounds) return sp;
+  int S = min(P / R, kSplitMaxS);
+  S = min(S, nk / 4);
+  if (S < 2) return sp;
+  sp.full = T - R;
+  sp.R = R;
+  sp.S = S;
   return sp;
 }
 // Workgroup b runs on XCD b % 8 (round-robin dispatch over the 8 XCDs of an
@@ -216,8 +227,10 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
   const int NP = static_cast<int>(gridDim.x), b = xcd_slot(static_cast<int>(blockIdx.x), NP);
   const int nk = args.K / BK;
   const SplitPlan sp = split_plan<MODE>(args, total_tiles, NP, nk);
-  if constexpr (MODE == DOWN_FWD || MODE == GATEUP_BWD) {
-    // descriptors of the split tiles for split_reduce_kernel (after the partials)
+  {
+    // descriptors of the split tiles for the split reduction (after the
+    // partials): first row, valid rows, first output column, valid columns
+    // (GATEUP_FWD: h columns, 128 per tile)
     if (args.split_ws != nullptr && threadIdx.x == 0) {
       int4* hdr = reinterpret_cast<int4*>(args.split_ws + static_cast<int64_t>(NP) * BM * BN);
       const int r = static_cast<int>(blockIdx.x);
@@ -225,7 +238,8 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
       if (r < sp.R) {
         int g, tm, tn, row_base, M;
         locate_tile(args, offsets, tiles_n, sp.full + r, g, tm, tn, row_base, M);
-        hdr[1 + r] = make_int4(row_base + tm * BM, min(M - tm * BM, BM), tn * BN, min(args.N - tn * BN, BN));
+        hdr[1 + r] = make_int4(row_base + tm * BM, min(M - tm * BM, BM), tn * TN_COLS,
+                               min(args.N - tn * TN_COLS, TN_COLS));
       }
     }
   }
@@ -487,32 +501,153 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
   }
 }
 
-// Sums the S fp32 partials of every K-split tile in range order and writes the
-// bf16 tile.  The product wrote, after the P tiles of partials, a header
-// {R, S} and one descriptor {first row, valid rows, first column, valid
-// columns} per split tile.  Block = (split tile r, eighth of its rows).
-__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ ws, int P,
-                                                           uint16_t* __restrict__ out, int64_t ldo) {
+// ---- split reductions
+// The product wrote, after the P tiles of partials, a header {R, S} and one
+// descriptor {first row, valid rows, first output column, valid output
+// columns} per split tile.  A reduction sums a split tile's S partials in
+// range order and writes the tile through the product's epilogue.  Block =
+// (split tile r, sixteenth of its rows); a thread takes units of 8
+// consecutive partial columns of one row.  Every partial slot is a whole
+// BM x BN region, so the loads need no bounds; only valid rows and columns
+// are stored.
+
+struct SplitTile {
+  bool active;
+  int S;
+  int4 d;
+  const float* src0;  // the tile's first partial
+};
+
+__device__ __forceinline__ SplitTile split_tile(const float* ws, int P) {
   using namespace core;
   const int4* hdr = reinterpret_cast<const int4*>(ws + static_cast<int64_t>(P) * BM * BN);
   const int4 h0 = hdr[0];
-  const int r = blockIdx.x / 8, part = blockIdx.x % 8;
-  if (r >= h0.x) return;
-  const int S = h0.y;
-  const int4 d = hdr[1 + r];
-  const float* src0 = ws + static_cast<int64_t>(r) * S * BM * BN;
-  // rows 32 part .. 32 part + 31 of the tile: 8192 outputs, 8 per thread and pass
-  for (int e0 = part * 32 * BN + threadIdx.x * 8; e0 < (part + 1) * 32 * BN; e0 += 256 * 8) {
-    const int row = e0 / BN, col = e0 % BN;
-    if (row >= d.y || col >= d.w) continue;
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int s = 0; s < S; ++s) {
-      const float4* src = reinterpret_cast<const float4*>(src0 + static_cast<int64_t>(s) * BM * BN + e0);
-      const float4 u = src[0], v = src[1];
-      acc[0] = acc[0] + u.x; acc[1] = acc[1] + u.y; acc[2] = acc[2] + u.z; acc[3] = acc[3] + u.w;
-      acc[4] = acc[4] + v.x; acc[5] = acc[5] + v.y; acc[6] = acc[6] + v.z; acc[7] = acc[7] + v.w;
+  const int r = blockIdx.x / kReduceParts;
+  SplitTile t;
+  t.active = r < h0.x;
+  t.S = h0.y;
+  t.d = t.active ? hdr[1 + r] : make_int4(0, 0, 0, 0);
+  t.src0 = ws + static_cast<int64_t>(r) * h0.y * BM * BN;
+  return t;
+}
+
+// Partial values o .. o + 7 of the S ranges, summed in range order from 0
+// (all kSplitMaxS loads issued first; ranges past S re-read range S - 1 and
+// are not added).
+__device__ __forceinline__ void sum_ranges8(const SplitTile& t, int o, float* acc) {
+  using namespace core;
+  float4 u[kSplitMaxS][2];
+#pragma unroll
+  for (int s = 0; s < kSplitMaxS; ++s) {
+    const float* p = t.src0 + static_cast<int64_t>(min(s, t.S - 1)) * BM * BN + o;
+    u[s][0] = *reinterpret_cast<const float4*>(p);
+    u[s][1] = *reinterpret_cast<const float4*>(p + 4);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < kSplitMaxS; ++s) {
+    const float v[8] = {u[s][0].x, u[s][0].y, u[s][0].z, u[s][0].w, u[s][1].x, u[s][1].y, u[s][1].z, u[s][1].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = (s < t.S) ? acc[e] + v[e] : acc[e];
+  }
+}
+
+// DOWN_FWD, GATEUP_BWD: the bf16 tile.  Two units per thread.
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ ws, int P,
+                                                           uint16_t* __restrict__ out, int64_t ldo) {
+  using namespace core;
+  const SplitTile t = split_tile(ws, P);
+  if (!t.active) return;
+  const int row0 = (blockIdx.x % kReduceParts) * 16;
+  float acc[2][8];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int u = threadIdx.x + q * 256;
+    sum_ranges8(t, (row0 + u / 32) * BN + (u % 32) * 8, acc[q]);
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int u = threadIdx.x + q * 256, row = row0 + u / 32, col = (u % 32) * 8;
+    if (row < t.d.y && col < t.d.w)
+      *reinterpret_cast<uint4*>(out + static_cast<int64_t>(t.d.x + row) * ldo + t.d.z + col) = pack8(acc[q]);
+  }
+}
+
+// GATEUP_FWD: a|b = bf16(acc), h = bf16(bf16(silu(a)) * b), as the tile
+// epilogue.  The partial columns of wave half w hold a for h columns
+// 64 w .. 64 w + 63, then b for the same columns.  One unit per thread.
+__global__ __launch_bounds__(256) void split_reduce_gateup_kernel(const GemmArgs args, int P) {
+  using namespace core;
+  const SplitTile t = split_tile(args.split_ws, P);
+  if (!t.active) return;
+  const int row = (blockIdx.x % kReduceParts) * 16 + threadIdx.x / 16, hc = (threadIdx.x % 16) * 8;
+  const int pa = (hc / 64) * 128 + hc % 64;
+  float a[8], b[8];
+  sum_ranges8(t, row * BN + pa, a);
+  sum_ranges8(t, row * BN + pa + 64, b);
+  if (row >= t.d.y || hc >= t.d.w) return;
+  const uint4 pka = pack8(a), pkb = pack8(b);
+  const int64_t grow = static_cast<int64_t>(t.d.x) + row;
+  const int col = t.d.z + hc;
+  store16(args.c0 + grow * args.ldc0 + col, pka, true);
+  store16(args.c0 + grow * args.ldc0 + args.inter + col, pkb, true);
+  float ar[8], br[8], hv[8];
+  unpack8(pka, ar);
+  unpack8(pkb, br);
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    float h0v = ar[e] * fast_sigmoid(ar[e]), h1v = ar[e + 1] * fast_sigmoid(ar[e + 1]);
+    bf_round2(h0v, h1v);
+    hv[e] = h0v * br[e];
+    hv[e + 1] = h1v * br[e + 1];
+  }
+  store16(args.c1 + grow * args.ldc1 + col, pack8(hv), true);
+}
+
+// DOWN_BWD: dh = bf16(acc), then the SwiGLU backward of the tile epilogue
+// with a|b read from args.aux (rows and columns clamped into the tile for
+// the loads).  Two units per thread.
+__global__ __launch_bounds__(256) void split_reduce_down_bwd_kernel(const GemmArgs args, int P) {
+  using namespace core;
+  const SplitTile t = split_tile(args.split_ws, P);
+  if (!t.active) return;
+  const int row0 = (blockIdx.x % kReduceParts) * 16;
+  float acc[2][8];
+  uint4 la[2], lb[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int u = threadIdx.x + q * 256, row = row0 + u / 32, c = (u % 32) * 8;
+    const int64_t lrow = static_cast<int64_t>(t.d.x) + min(row, t.d.y - 1);
+    const uint16_t* src = args.aux + lrow * args.ldaux + t.d.z + min(c, t.d.w - 8);
+    la[q] = load16(src, true);
+    lb[q] = load16(src + args.inter, true);
+    sum_ranges8(t, row * BN + c, acc[q]);
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int u = threadIdx.x + q * 256, row = row0 + u / 32, c = (u % 32) * 8;
+    if (row >= t.d.y || c >= t.d.w) continue;
+    const int64_t grow = static_cast<int64_t>(t.d.x) + row;
+    const int hc = t.d.z + c;
+    float dh[8], af[8], bfv[8], da[8], db[8];
+    unpack8(pack8(acc[q]), dh);  // dh arrives bf16-rounded, as in the tile epilogue
+    unpack8(la[q], af);
+    unpack8(lb[q], bfv);
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const float sg0 = fast_sigmoid(af[e]), sg1 = fast_sigmoid(af[e + 1]);
+      const float sa0 = af[e] * sg0, sa1 = af[e + 1] * sg1;
+      float sv0 = sa0, sv1 = sa1, ds0 = dh[e] * bfv[e], ds1 = dh[e + 1] * bfv[e + 1];
+      bf_round2(sv0, sv1);
+      bf_round2(ds0, ds1);
+      da[e] = ds0 * fmaf(sa0, 1.0f - sg0, sg0);
+      da[e + 1] = ds1 * fmaf(sa1, 1.0f - sg1, sg1);
+      db[e] = dh[e] * sv0;
+      db[e + 1] = dh[e + 1] * sv1;
     }
-    *reinterpret_cast<uint4*>(out + static_cast<int64_t>(d.x + row) * ldo + d.z + col) = pack8(acc);
+    store16(args.c0 + grow * args.ldc0 + hc, pack8(da), true);
+    store16(args.c0 + grow * args.ldc0 + args.inter + hc, pack8(db), true);
   }
 }
 
@@ -1090,11 +1225,22 @@ int launch_rows(GemmArgs& a, int64_t rows_routed, int64_t rows_shared, int E, vo
   if (tiles <= 0) return FMOE_OK;
   if (!all_small) {
     const int64_t grid = tiles < device_cus() ? tiles : device_cus();
+    // A run of kSplitMaxRounds full rounds or more never splits (split_plan);
+    // sum over groups of ceil(M_g / BM) >= ceil(rows / BM) bounds the tile
+    // count from below, so such a run skips the header and the reduction.
+    const int64_t tiles_lo = (ceil_div(rows_routed, core::BM) + ceil_div(rows_shared, core::BM)) * tiles_n;
+    if (a.small_max == 0 && tiles_lo / grid >= kSplitMaxRounds) a.split_ws = nullptr;
     rows_gemm_kernel<MODE><<<dim3(grid), dim3(core::NT), 0, as_stream(stream)>>>(a, a.offsets);
-    if constexpr (MODE == DOWN_FWD || MODE == GATEUP_BWD) {
-      if (a.split_ws != nullptr)
-        split_reduce_kernel<<<dim3(grid * 8), dim3(256), 0, as_stream(stream)>>>(a.split_ws, static_cast<int>(grid),
-                                                                                 a.c0, a.ldc0);
+    if (a.split_ws != nullptr) {
+      if constexpr (MODE == DOWN_FWD || MODE == GATEUP_BWD)
+        split_reduce_kernel<<<dim3(grid * kReduceParts), dim3(256), 0, as_stream(stream)>>>(
+            a.split_ws, static_cast<int>(grid), a.c0, a.ldc0);
+      else if constexpr (MODE == GATEUP_FWD)
+        split_reduce_gateup_kernel<<<dim3(grid * kReduceParts), dim3(256), 0, as_stream(stream)>>>(
+            a, static_cast<int>(grid));
+      else
+        split_reduce_down_bwd_kernel<<<dim3(grid * kReduceParts), dim3(256), 0, as_stream(stream)>>>(
+            a, static_cast<int>(grid));
     }
   }
   if constexpr (kHasSmall) {
@@ -1134,10 +1280,15 @@ void fill_groups(GemmArgs& a, const int32_t* offsets, int E, int64_t rows_routed
 
 using namespace fmoe;
 
+extern "C" size_t fmoe_split_workspace_bytes(void) {
+  const size_t P = static_cast<size_t>(device_cus());
+  return P * core::BM * core::BN * sizeof(float) + (P + 1) * 16;  // partials + descriptors
+}
+
 extern "C" int fmoe_gateup_fwd(const void* x_routed, const void* x_shared, const int32_t* offsets,
                                int n_experts, int64_t rows_routed, int64_t rows_shared, int64_t dim,
                                int64_t inter, const void* const* w1, const void* const* w3,
-                               void* ab, void* h, void* stream) {
+                               void* ab, void* h, void* workspace, size_t workspace_bytes, void* stream) {
   int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
   if (st) return st;
   if (rows_routed + rows_shared == 0) return FMOE_OK;
@@ -1158,6 +1309,7 @@ extern "C" int fmoe_gateup_fwd(const void* x_routed, const void* x_shared, const
   a.c1 = static_cast<uint16_t*>(h);
   a.ldc0 = 2 * inter;
   a.ldc1 = inter;
+  a.split_ws = (workspace && workspace_bytes >= fmoe_split_workspace_bytes()) ? static_cast<float*>(workspace) : nullptr;
   const int G = n_experts + (rows_shared > 0 ? 1 : 0);
   for (int g = 0; g < G; ++g) {
     if (!w1[g] || !w3[g]) return FMOE_ERR_INVALID_ARG;
@@ -1165,11 +1317,6 @@ extern "C" int fmoe_gateup_fwd(const void* x_routed, const void* x_shared, const
     a.b1[g] = static_cast<const uint16_t*>(w3[g]);
   }
   return launch_rows<GATEUP_FWD>(a, rows_routed, rows_shared, n_experts, stream);
-}
-
-extern "C" size_t fmoe_split_workspace_bytes(void) {
-  const size_t P = static_cast<size_t>(device_cus());
-  return P * core::BM * core::BN * sizeof(float) + (P + 1) * 16;  // partials + descriptors
 }
 
 extern "C" int fmoe_down_fwd(const void* h, const int32_t* offsets, int n_experts,
@@ -1204,7 +1351,8 @@ extern "C" int fmoe_down_fwd(const void* h, const int32_t* offsets, int n_expert
 extern "C" int fmoe_down_bwd_dx(const void* d_out_routed, const void* d_out_shared,
                                 const int32_t* offsets, int n_experts, int64_t rows_routed,
                                 int64_t rows_shared, int64_t dim, int64_t inter, const void* w2t,
-                                const void* ab, void* d_ab, void* stream) {
+                                const void* ab, void* d_ab, void* workspace, size_t workspace_bytes,
+                                void* stream) {
   int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
   if (st) return st;
   if (rows_routed + rows_shared == 0) return FMOE_OK;
@@ -1225,6 +1373,7 @@ extern "C" int fmoe_down_bwd_dx(const void* d_out_routed, const void* d_out_shar
   a.ldc0 = 2 * inter;
   a.aux = static_cast<const uint16_t*>(ab);
   a.ldaux = 2 * inter;
+  a.split_ws = (workspace && workspace_bytes >= fmoe_split_workspace_bytes()) ? static_cast<float*>(workspace) : nullptr;
   const int G = n_experts + (rows_shared > 0 ? 1 : 0);
   for (int g = 0; g < G; ++g) a.b0[g] = static_cast<const uint16_t*>(w2t) + static_cast<int64_t>(g) * inter * dim;
   return launch_rows<DOWN_BWD>(a, rows_routed, rows_shared, n_experts, stream);

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define FMOE_ABI_VERSION 9
+#define FMOE_ABI_VERSION 10
 #define FMOE_MAX_EXPERTS 64
 #define FMOE_MAX_TOPK 8
 #define FMOE_MAX_CAST 64
@@ -159,19 +159,24 @@ int fmoe_route_and_dispatch(const void* x, const void* gate_w, const void* gate_
  * x_routed: [rows_routed, dim] (x_perm from fmoe_dispatch); x_shared: [T, dim].
  * Outputs over all rows: ab [rows, 2*inter] (a in columns 0..inter-1, b in
  * inter..2*inter-1; kept for the backward pass), h [rows, inter].
+ * workspace: see fmoe_split_workspace_bytes.
  * ------------------------------------------------------------------------- */
 int fmoe_gateup_fwd(const void* x_routed, const void* x_shared,
                     const int32_t* offsets, int n_experts,
                     int64_t rows_routed, int64_t rows_shared,
                     int64_t dim, int64_t inter,
                     const void* const* w1, const void* const* w3,
-                    void* ab, void* h, void* stream);
+                    void* ab, void* h, void* workspace, size_t workspace_bytes,
+                    void* stream);
 
-/* Workspace of the plain-output products (fmoe_down_fwd, fmoe_gateup_bwd_dx)
- * for the current device: fp32 partials of the tiles of the last, partial
- * round of the persistent grid, which are split along K (up to 4 ranges) and
- * summed in range order (deterministic).  Passing no (or a smaller) workspace
- * runs those tiles whole. */
+/* Workspace of the four row products (fmoe_gateup_fwd, fmoe_down_fwd,
+ * fmoe_down_bwd_dx, fmoe_gateup_bwd_dx) for the current device: fp32
+ * partials of the tiles of the last, partial round of the persistent grid,
+ * which are split along K (up to 4 ranges), summed in range order
+ * (deterministic) and then put through the product's epilogue, with the
+ * same rounding points as a whole tile.  Passing no (or a smaller)
+ * workspace runs those tiles whole.  Calls that share one workspace must
+ * not overlap. */
 size_t fmoe_split_workspace_bytes(void);
 
 /* Grouped down projection w2(h) of SwiGLUExpert.forward (models/moe.py:21),
@@ -227,12 +232,14 @@ int fmoe_transpose_weights(const void* const* w1, const void* const* w3,
 /* dh = d_out w2 (bf16-rounded), then the SwiGLU backward in the epilogue:
  *   da = bf16(bf16(dh*b) * silu'(a)),  db = bf16(dh * bf16(silu(a))).
  * d_out_routed: [rows_routed, dim]; d_out_shared: [rows_shared, dim];
- * ab from fmoe_gateup_fwd; d_ab: [rows, 2*inter]. */
+ * ab from fmoe_gateup_fwd; d_ab: [rows, 2*inter];
+ * workspace: see fmoe_split_workspace_bytes. */
 int fmoe_down_bwd_dx(const void* d_out_routed, const void* d_out_shared,
                      const int32_t* offsets, int n_experts,
                      int64_t rows_routed, int64_t rows_shared,
                      int64_t dim, int64_t inter, const void* w2t,
-                     const void* ab, void* d_ab, void* stream);
+                     const void* ab, void* d_ab, void* workspace, size_t workspace_bytes,
+                     void* stream);
 
 /* dx_rows = da w1 + db w3 for every row (one product over K = 2*inter);
  * dx_rows: [rows, dim] bf16; workspace: see fmoe_split_workspace_bytes. */

@@ -408,6 +408,83 @@ def test_backward_products(gpu_device, counts, shared, d, I):
         assert rel_l2(dw3[grp].cpu(), dw3_ref) < 1e-5
 
 
+def _row_products(D, x_r, x_s, do_r, do_s, offsets, E, w1, w3, w2, w13t, w2t, ab_in, h_in, dab_in, split):
+    """The four row products through the C ABI, with the split workspace or
+    without it; each product reads fixed inputs (not the previous product's
+    output), so only its own summation order differs between the two runs."""
+    from fusionllm_amd import _lib
+    lib = _lib.load()
+    rows_r, d = x_r.shape
+    rows_s = x_s.shape[0]
+    I = w1[0].shape[0]
+    rows = rows_r + rows_s
+    ws_bytes = lib.fmoe_split_workspace_bytes() if split else 0
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=D)
+    wsp = ws.data_ptr() if split else None
+    pa = lambda ts: _lib.ptr_array([t.data_ptr() for t in ts])
+    st = K._stream()
+    ab = torch.empty(rows, 2 * I, dtype=torch.bfloat16, device=D)
+    h = torch.empty(rows, I, dtype=torch.bfloat16, device=D)
+    _lib.check(lib.fmoe_gateup_fwd(x_r.data_ptr(), x_s.data_ptr(), offsets.data_ptr(), E, rows_r, rows_s, d, I,
+                                   pa(w1), pa(w3), ab.data_ptr(), h.data_ptr(), wsp, ws_bytes, st), "gateup_fwd")
+    o = torch.empty(rows, d, dtype=torch.bfloat16, device=D)
+    _lib.check(lib.fmoe_down_fwd(h_in.data_ptr(), offsets.data_ptr(), E, rows_r, rows_s, d, I, pa(w2),
+                                 o.data_ptr(), wsp, ws_bytes, st), "down_fwd")
+    d_ab = torch.empty(rows, 2 * I, dtype=torch.bfloat16, device=D)
+    _lib.check(lib.fmoe_down_bwd_dx(do_r.data_ptr(), do_s.data_ptr(), offsets.data_ptr(), E, rows_r, rows_s, d, I,
+                                    w2t.data_ptr(), ab_in.data_ptr(), d_ab.data_ptr(), wsp, ws_bytes, st),
+               "down_bwd_dx")
+    dx = torch.empty(rows, d, dtype=torch.bfloat16, device=D)
+    _lib.check(lib.fmoe_gateup_bwd_dx(dab_in.data_ptr(), offsets.data_ptr(), E, rows_r, rows_s, d, I,
+                                      w13t.data_ptr(), dx.data_ptr(), wsp, ws_bytes, st), "gateup_bwd_dx")
+    return [t.cpu() for t in (ab, h, o, d_ab, dx)]
+
+
+def test_split_tail_matches_whole_tiles(gpu_device):
+    """The last, partial round of the persistent grid split along K (summed in
+    range order, then the product's own epilogue) against the same tiles run
+    whole.  26000 rows of d=768, I=2048 put every product's tile count above
+    the 256-CU grid with a remainder: gate/up 1664 tiles, down 312, down
+    backward 832, gate/up backward 312.  Only the fp32 summation order of the
+    split tiles differs: an output agrees with the whole-tile one to a few
+    bf16 roundings (one on the sum, up to three more through the SwiGLU
+    epilogues, each at most 2^-7 relative), and every row of the first group
+    (tiles of the first rounds) is bit-identical."""
+    D = gpu_device
+    g = torch.Generator().manual_seed(7)
+    counts, shared, d, I = [6000, 6000, 6000, 6000], 2000, 768, 2048
+    E = len(counts)
+    offsets, rows_r = _groups(counts, D)
+    G = E + 1
+    x_r, x_s = _bf(rows_r, d, g=g).to(D), _bf(shared, d, g=g).to(D)
+    do_r, do_s = _bf(rows_r, d, g=g).to(D), _bf(shared, d, g=g).to(D)
+    ab_in = _bf(rows_r + shared, 2 * I, g=g).to(D)
+    h_in = _bf(rows_r + shared, I, scale=0.3, g=g).to(D)
+    dab_in = _bf(rows_r + shared, 2 * I, scale=0.05, g=g).to(D)
+    w1 = [_bf(I, d, scale=0.05, g=g).to(D) for _ in range(G)]
+    w3 = [_bf(I, d, scale=0.05, g=g).to(D) for _ in range(G)]
+    w2 = [_bf(d, I, scale=0.05, g=g).to(D) for _ in range(G)]
+    w13t, w2t = K.transpose_weights(w1, w3, w2)
+    args = (D, x_r, x_s, do_r, do_s, offsets, E, w1, w3, w2, w13t, w2t, ab_in, h_in, dab_in)
+    split = _row_products(*args, split=True)
+    whole = _row_products(*args, split=False)
+    names = ("ab", "h", "out", "d_ab", "dx_rows")
+    for name, a, b in zip(names, split, whole):
+        assert torch.equal(a[:counts[0]], b[:counts[0]]), name
+        close(a, b, rtol=3.2e-2, atol=2e-3)
+        assert rel_l2(a, b.float()) < 2e-3, name
+    # and the split outputs against fp32 products of the shared group's rows
+    # (the last tiles in tile order, where the split round lands)
+    xs = x_s.cpu().float()
+    a_ref = xs @ w1[E].cpu().float().T
+    close(split[0][rows_r:, :I], a_ref, rtol=8e-3, atol=1e-3)
+    o_ref = h_in[rows_r:].cpu().float() @ w2[E].cpu().float().T
+    close(split[2][rows_r:], o_ref, rtol=8e-3, atol=1e-3)
+    dag, dbg = dab_in[rows_r:, :I].cpu().float(), dab_in[rows_r:, I:].cpu().float()
+    dx_ref = dag @ w1[E].cpu().float() + dbg @ w3[E].cpu().float()
+    close(split[4][rows_r:], dx_ref, rtol=1e-2, atol=2e-3)
+
+
 @pytest.mark.parametrize("G,d,I", [(9, 768, 2048), (2, 64, 192), (3, 192, 64)])
 def test_transpose_weights_bit_exact(gpu_device, G, d, I):
     g = torch.Generator().manual_seed(G)

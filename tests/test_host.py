@@ -54,8 +54,8 @@ def test_argument_errors_without_gpu():
     assert lib.fmoe_dispatch_noalloc(None, None, 87382, 2048, 64, 6, None, None, None, None, None, None) == 8
     assert b"1 MiB" in lib.fmoe_status_string(8)
     pp = _lib.ptr_array([0])
-    assert lib.fmoe_gateup_fwd(None, None, None, 1, 10, 0, 96, 128, pp, pp, None, None, None) == 2
-    assert lib.fmoe_gateup_fwd(None, None, None, 1, 10, 0, 128, 128, pp, pp, None, None, None) == 1
+    assert lib.fmoe_gateup_fwd(None, None, None, 1, 10, 0, 96, 128, pp, pp, None, None, None, 0, None) == 2
+    assert lib.fmoe_gateup_fwd(None, None, None, 1, 10, 0, 128, 128, pp, pp, None, None, None, 0, None) == 1
     assert lib.fmoe_combine_fwd(None, None, None, None, 4, 768, 2, 8, 1, 5, None, None, None) == 4
     # RMSNorm around the block
     assert lib.fmoe_rmsnorm_fwd(None, 0, None, 0, 4, 100, 1e-6, None, None, None) == 2
