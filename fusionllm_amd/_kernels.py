@@ -122,11 +122,22 @@ def route_dispatch(x, gate_w, gate_b, k: int, route_scale: float):
     return idx, idx64, w, v, counts, offsets, perm, pos, x_perm
 
 
+def _host_counts(counts_host, E):
+    if counts_host is None:
+        return None
+    if (counts_host.device.type != "cpu" or not counts_host.is_pinned() or counts_host.dtype != torch.int32
+            or counts_host.numel() < E or not counts_host.is_contiguous()):
+        raise RuntimeError("counts_host must be a contiguous pinned int32 CPU tensor of at least n_experts")
+    return counts_host.data_ptr()
+
+
 @_timed
-def route_and_dispatch(x, gate_w, gate_b, k: int, route_scale: float, gather: bool = True):
+def route_and_dispatch(x, gate_w, gate_b, k: int, route_scale: float, gather: bool = True,
+                       counts_host: torch.Tensor | None = None):
     """router_fwd followed by dispatch for any T, in three launches (the router counts the
     dispatch histogram, the scatter copies the rows); returns idx32, idx64, weights, topv,
-    counts, offsets, perm, pos, x_perm."""
+    counts, offsets, perm, pos, x_perm.  counts_host: optional pinned int32 [E] tensor that
+    also receives the expert counts (readable after the stream has passed this call)."""
     lib = _lib.load()
     T, d = x.shape
     E = gate_w.shape[0]
@@ -147,7 +158,7 @@ def route_and_dispatch(x, gate_w, gate_b, k: int, route_scale: float, gather: bo
                                       idx.data_ptr(), idx64.data_ptr(), w.data_ptr(), v.data_ptr(),
                                       counts.data_ptr(), offsets.data_ptr(), perm.data_ptr(), pos.data_ptr(),
                                       x_perm.data_ptr() if x_perm is not None else None,
-                                      ws.data_ptr(), ws_bytes, _stream()),
+                                      _host_counts(counts_host, E), ws.data_ptr(), ws_bytes, _stream()),
           "fmoe_route_and_dispatch")
     return idx, idx64, w, v, counts, offsets, perm, pos, x_perm
 

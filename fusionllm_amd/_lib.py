@@ -13,7 +13,7 @@ from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int64, c_size_
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libfusionmoe.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 MAX_EXPERTS = 64
 MAX_TOPK = 8
 
@@ -36,7 +36,7 @@ SIGNATURES = {
     "fmoe_dispatch_noalloc": (c_int, [_P, _P, c_int64, c_int64, c_int, c_int, _P, _P, _P, _P, _P, _P]),
     "fmoe_route_and_dispatch_workspace_bytes": (c_size_t, [c_int64, c_int, c_int]),
     "fmoe_route_and_dispatch": (c_int, [_P, _P, _P, c_int64, c_int64, c_int, c_int, c_float,
-                                        _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_size_t, _P]),
+                                        _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_size_t, _P]),
     "fmoe_gateup_fwd": (c_int, [_P, _P, _P, c_int, c_int64, c_int64, c_int64, c_int64,
                                 _PP, _PP, _P, _P, _P, c_size_t, _P]),
     "fmoe_split_workspace_bytes": (c_size_t, []),

@@ -71,9 +71,16 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
   return v;
 }
 
+// The expert counts also go to counts_host (nullable): host memory that the
+// caller reads once the stream has passed this kernel, written with
+// system-scope stores (through to memory, visible to the host).
+__device__ __forceinline__ void store_host(int32_t* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 __global__ __launch_bounds__(kScanThreads) void dispatch_scan_kernel(
     const int32_t* __restrict__ block_hist, int nblocks, int E, int32_t* __restrict__ block_base,
-    int32_t* __restrict__ counts, int32_t* __restrict__ offsets) {
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ counts_host) {
   __shared__ int total[FMOE_MAX_EXPERTS];
   __shared__ int start[FMOE_MAX_EXPERTS + 1];
   __shared__ int wsum[kScanWaves][64];
@@ -109,6 +116,7 @@ __global__ __launch_bounds__(kScanThreads) void dispatch_scan_kernel(
         start[lane] = incl - t;
         counts[lane] = t;
         offsets[lane] = incl - t;
+        if (counts_host) store_host(counts_host + lane, t);
       }
       if (lane == 63) {
         start[E] = incl;
@@ -159,6 +167,7 @@ __global__ __launch_bounds__(kScanThreads) void dispatch_scan_kernel(
   for (int e = threadIdx.x; e < E; e += kScanThreads) {
     counts[e] = total[e];
     offsets[e] = start[e];
+    if (counts_host) store_host(counts_host + e, total[e]);
   }
   if (threadIdx.x == 0) offsets[E] = start[E];
   for (int e = wave; e < E; e += nwaves) {
@@ -448,7 +457,7 @@ extern "C" int fmoe_dispatch(const int32_t* idx, const void* x, int64_t T, int64
   const int64_t nblocks = ceil_div(n_slots, kSlotsPerBlock);
   if (T == 0) {
     // Empty batch: every count and offset is zero (scan over zero blocks).
-    dispatch_scan_kernel<<<1, kScanThreads, 0, s>>>(nullptr, 0, n_experts, nullptr, counts, offsets);
+    dispatch_scan_kernel<<<1, kScanThreads, 0, s>>>(nullptr, 0, n_experts, nullptr, counts, offsets, nullptr);
     return launch_status();
   }
   if (!idx || !x || !perm || !pos_of_slot || !workspace) return FMOE_ERR_INVALID_ARG;
@@ -467,7 +476,7 @@ extern "C" int fmoe_dispatch(const int32_t* idx, const void* x, int64_t T, int64
   dispatch_hist_kernel<<<dim3(nblocks), dim3(kDispThreads), 0, s>>>(idx, (int)n_slots, n_experts,
                                                                    block_hist);
   dispatch_scan_kernel<<<1, kScanThreads, 0, s>>>(block_hist, (int)nblocks, n_experts, block_base,
-                                                  counts, offsets);
+                                                  counts, offsets, nullptr);
   dispatch_scatter_kernel<<<dim3(nblocks), dim3(kDispThreads), 0, s>>>(
       idx, (int)n_slots, n_experts, block_base, perm, pos_of_slot);
   if (x_perm) {
@@ -505,7 +514,8 @@ extern "C" int fmoe_route_and_dispatch(const void* x, const void* gate_w, const 
                                        int64_t dim, int n_experts, int k, float route_scale, int32_t* idx,
                                        int64_t* idx64, float* weights, float* topv, int32_t* counts,
                                        int32_t* offsets, int32_t* perm, int32_t* pos_of_slot, void* x_perm,
-                                       void* workspace, size_t workspace_bytes, void* stream) {
+                                       int32_t* counts_host, void* workspace, size_t workspace_bytes,
+                                       void* stream) {
   if (T < 0 || dim <= 0) return FMOE_ERR_INVALID_ARG;
   if (n_experts <= 0 || n_experts > FMOE_MAX_EXPERTS) return FMOE_ERR_TOO_MANY_EXPERTS;
   if (k <= 0 || k > FMOE_MAX_TOPK || k > n_experts || dim % 64 != 0 || dim > 2048) return FMOE_ERR_SHAPE;
@@ -514,7 +524,7 @@ extern "C" int fmoe_route_and_dispatch(const void* x, const void* gate_w, const 
   hipStream_t s = as_stream(stream);
   if (T == 0) {
     // no tokens: empty experts (the scan over zero blocks writes counts 0, offsets 0)
-    dispatch_scan_kernel<<<1, kScanThreads, 0, s>>>(nullptr, 0, n_experts, nullptr, counts, offsets);
+    dispatch_scan_kernel<<<1, kScanThreads, 0, s>>>(nullptr, 0, n_experts, nullptr, counts, offsets, counts_host);
     return launch_status();
   }
   if (!x || !gate_w || !gate_b || !idx || !weights || !topv || !perm || !pos_of_slot) return FMOE_ERR_INVALID_ARG;
@@ -528,11 +538,14 @@ extern "C" int fmoe_route_and_dispatch(const void* x, const void* gate_w, const 
                               static_cast<const uint16_t*>(gate_b), T, dim, n_experts, k, route_scale, idx, idx64,
                               weights, topv, block_hist, s);
   if (st) return st;
-  dispatch_scan_kernel<<<1, kScanThreads, 0, s>>>(block_hist, static_cast<int>(nblocks), n_experts, block_base,
-                                                   counts, offsets);
   const int64_t nsplit = x_perm ? ceil_div(static_cast<int64_t>(kRouteBlockTokens) * (dim / 8), kCopyPerWG) : 1;
-  dispatch_scatter_copy_kernel<<<dim3(nblocks, nsplit), dim3(kDispThreads), 0, s>>>(
-      idx, static_cast<int>(T * k), kRouteBlockTokens * k, n_experts, k, block_base,
-      static_cast<const uint4*>(x), static_cast<int>(dim / 8), perm, pos_of_slot, static_cast<uint4*>(x_perm));
+  const dim3 grid(static_cast<unsigned>(nblocks), static_cast<unsigned>(nsplit));
+  const int n_slots = static_cast<int>(T * k), spb = kRouteBlockTokens * k, chunks = static_cast<int>(dim / 8);
+  const uint4* xs = static_cast<const uint4*>(x);
+  uint4* xp = static_cast<uint4*>(x_perm);
+  dispatch_scan_kernel<<<1, kScanThreads, 0, s>>>(block_hist, static_cast<int>(nblocks), n_experts, block_base,
+                                                   counts, offsets, counts_host);
+  dispatch_scatter_copy_kernel<<<grid, dim3(kDispThreads), 0, s>>>(idx, n_slots, spb, n_experts, k, block_base, xs,
+                                                                 chunks, perm, pos_of_slot, xp);
   return launch_status();
 }

@@ -38,6 +38,7 @@ input of different dtypes outside autocast raise, as the reference's
 """
 from __future__ import annotations
 
+import collections
 import contextlib
 
 import torch
@@ -218,10 +219,13 @@ class DenseFFN(SwiGLUExpert):
     one-group kernels."""
 
 
-def _forward_pass(meta, x, gate_w, gate_b, weights, residual=None):
+def _forward_pass(meta, x, gate_w, gate_b, weights, residual=None, counts_host=None):
     """The forward kernels of DeepSeekMoE.forward (models/moe.py:79-87); returns
     the output and every intermediate the backward pass needs.  With a
-    residual the output is residual + moe(x) (models/fusionllm.py:52)."""
+    residual the output is residual + moe(x) (models/fusionllm.py:52).
+    counts_host (pinned int32 [E], optional) receives the expert counts
+    asynchronously: written by the routing kernel itself on the
+    route_and_dispatch path, by a copy on the others."""
     E, k, inter, rs, has_shared, out_dtype = meta
     T, d = x.shape
     xb, gwb, gbb, *wb = _bf16_operands([x, gate_w, gate_b, *weights])
@@ -235,10 +239,15 @@ def _forward_pass(meta, x, gate_w, gate_b, weights, residual=None):
         # routing with the dispatch histogram, scan, scatter with the row copies: three launches.
         # Up to ROUTER_SMALL_T tokens the router's one-workgroup-per-token kernel and the
         # one-launch small dispatch below are faster (C3 replay at 32 tokens: 49 against 55 us).
-        idx, idx64, w, v, counts, offsets, perm, pos, x_perm = K.route_and_dispatch(xb, gwb, gbb, k, rs)
+        # The expert counts reach counts_host from the kernel itself.
+        idx, idx64, w, v, counts, offsets, perm, pos, x_perm = K.route_and_dispatch(
+            xb, gwb, gbb, k, rs, counts_host=counts_host)
+        counts_host = None
     else:
         idx, idx64, w, v = K.router_fwd(xb, gwb, gbb, k, rs)
         counts, offsets, perm, pos, x_perm = K.dispatch(idx, xb, E)
+    if counts_host is not None:
+        counts_host.copy_(counts, non_blocking=True)
     rows_r, rows_s = T * k, (T if has_shared else 0)
     ab, h = K.gateup_fwd(x_perm, xb if has_shared else None, offsets, E, w1s, w3s, inter)
     o = K.down_fwd(h, offsets, E, rows_r, rows_s, w2s, d)
@@ -246,18 +255,35 @@ def _forward_pass(meta, x, gate_w, gate_b, weights, residual=None):
     return xb, gwb, wb, idx, idx64, w, v, counts, offsets, perm, pos, x_perm, ab, h, o, y
 
 
-def _save_forward(ctx, meta, fw, gate_w, gate_b, weights):
+def _host_counts(meta):
+    """Pinned host buffer for the forward's expert counts (filled
+    asynchronously by _forward_pass and read at the end of backward)."""
+    return torch.empty(meta[0], dtype=torch.int32, pin_memory=True)
+
+
+# (event, pinned tensor) pairs: a kernel writes the tensor before the event
+# completes, and torch's caching host allocator does not know of that write,
+# so the tensor is held here (and not handed out again) until then, also when
+# the autograd context that owns it is dropped early (no backward).
+_pending_host_writes = collections.deque()
+
+
+def _hold_until(ev, t):
+    while _pending_host_writes and _pending_host_writes[0][0].query():
+        _pending_host_writes.popleft()
+    _pending_host_writes.append((ev, t))
+
+
+def _save_forward(ctx, meta, fw, gate_w, gate_b, weights, counts_host):
     """Keep what the backward kernels read; the expert counts travel to the
-    host asynchronously and are read at the end of backward.  Returns the
-    tensors to save."""
-    E = meta[0]
+    host asynchronously (counts_host, given to _forward_pass) and are read at
+    the end of backward.  Returns the tensors to save."""
     xb, gwb, wb, idx, idx64, w, v, counts, offsets, perm, pos, x_perm, ab, h, o, y = fw
     # Experts that get no tokens return None gradients (the reference never
     # puts them in the graph, moe.py:66-72).
-    counts_host = torch.empty(E, dtype=torch.int32, pin_memory=True)
-    counts_host.copy_(counts, non_blocking=True)
     ev = torch.cuda.Event()
     ev.record()
+    _hold_until(ev, counts_host)
     ctx.meta = meta
     ctx.counts_host = counts_host
     ctx.counts_event = ev
@@ -332,9 +358,10 @@ class _MoEBlockFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, meta, x, gate_w, gate_b, *weights):
-        fw = _forward_pass(meta, x, gate_w, gate_b, weights)
+        counts_host = _host_counts(meta)
+        fw = _forward_pass(meta, x, gate_w, gate_b, weights, counts_host=counts_host)
         ctx.x_dtype = x.dtype
-        ctx.save_for_backward(*_save_forward(ctx, meta, fw, gate_w, gate_b, weights))
+        ctx.save_for_backward(*_save_forward(ctx, meta, fw, gate_w, gate_b, weights, counts_host))
         idx64, w, counts, y = fw[4], fw[5], fw[7], fw[-1]
         return y, idx64, w, counts
 
@@ -367,8 +394,9 @@ class _NormMoEResidualFunction(torch.autograd.Function):
         xc = x.contiguous()
         nw = None if norm_w is None else norm_w.contiguous()
         xn, rstd = K.rmsnorm_fwd(xc, nw, eps)
-        fw = _forward_pass(meta, xn, gate_w, gate_b, weights, residual=xc)
-        saved = _save_forward(ctx, meta, fw, gate_w, gate_b, weights)
+        counts_host = _host_counts(meta)
+        fw = _forward_pass(meta, xn, gate_w, gate_b, weights, residual=xc, counts_host=counts_host)
+        saved = _save_forward(ctx, meta, fw, gate_w, gate_b, weights, counts_host)
         ctx.has_norm_w = nw is not None
         ctx.save_for_backward(xc, rstd, nw, *saved)
         idx64, w, counts, y = fw[4], fw[5], fw[7], fw[-1]

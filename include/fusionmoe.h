@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define FMOE_ABI_VERSION 10
+#define FMOE_ABI_VERSION 11
 #define FMOE_MAX_EXPERTS 64
 #define FMOE_MAX_TOPK 8
 #define FMOE_MAX_CAST 64
@@ -135,18 +135,21 @@ int fmoe_route_dispatch(const void* x, const void* gate_w, const void* gate_b,
  * launches instead of five: the router kernel of fmoe_router_fwd also counts
  * each workgroup's choices per expert (the dispatch histogram over blocks of
  * 32 tokens), one workgroup scans the counts, and the stable counting-sort
- * scatter copies each block's rows into x_perm itself.  The outputs are those
- * of fmoe_router_fwd followed by fmoe_dispatch on its idx, bit for bit.
- * dim <= 2048; x_perm may be NULL (no gather); workspace: see the query
- * (2 * ceil(T / 32) * E int32).  Meant for more than 128 tokens: up to 128,
- * fmoe_router_fwd (one workgroup per token) and fmoe_dispatch (one launch up
- * to 256 slots) are faster. */
+ * scatter copies each block's rows into x_perm itself.
+ * The outputs are those of fmoe_router_fwd followed by fmoe_dispatch on its
+ * idx, bit for bit.  counts_host (nullable): E int32 of pinned host memory
+ * that also receives the expert counts (the host copy the module reads in
+ * its backward, models/moe.py:66-72's skip of experts without tokens),
+ * readable once the stream has passed this call.  dim <= 2048; x_perm may be
+ * NULL (no gather); workspace: see the query (2 * ceil(T / 32) * E int32).
+ * Meant for more than 128 tokens: up to 128, fmoe_router_fwd (one workgroup
+ * per token) and fmoe_dispatch (one launch up to 256 slots) are faster. */
 size_t fmoe_route_and_dispatch_workspace_bytes(int64_t T, int n_experts, int k);
 int fmoe_route_and_dispatch(const void* x, const void* gate_w, const void* gate_b,
                             int64_t T, int64_t dim, int n_experts, int k, float route_scale,
                             int32_t* idx, int64_t* idx64, float* weights, float* topv,
                             int32_t* counts, int32_t* offsets, int32_t* perm,
-                            int32_t* pos_of_slot, void* x_perm,
+                            int32_t* pos_of_slot, void* x_perm, int32_t* counts_host,
                             void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------

@@ -113,7 +113,10 @@ def test_route_and_dispatch_equals_router_then_dispatch(gpu_device, T, d, E, k, 
     # copies) against fmoe_router_fwd + fmoe_dispatch and the C oracle: every output bit-equal
     x, gw, gb = _routing_inputs(T, d, E, seed=T + 3 * E)
     xd, gwd, gbd = x.to(gpu_device), gw.to(gpu_device), gb.to(gpu_device)
-    got = K.route_and_dispatch(xd, gwd, gbd, k, rs)
+    counts_host = torch.full((E,), -1, dtype=torch.int32).pin_memory()
+    got = K.route_and_dispatch(xd, gwd, gbd, k, rs, counts_host=counts_host)
+    torch.cuda.synchronize()
+    assert torch.equal(counts_host, got[4].cpu())  # the host copy written by the kernel
     idx, idx64, w, v = K.router_fwd(xd, gwd, gbd, k, rs)
     ref = (idx, idx64, w, v) + tuple(K.dispatch(idx, xd, E))
     names = ("idx", "idx64", "weights", "topv", "counts", "offsets", "perm", "pos", "x_perm")
@@ -145,7 +148,10 @@ def test_route_and_dispatch_degenerate_routing(gpu_device, case):
         gb = torch.full_like(gb, -20.0)
         gb[5] = 20.0
     xd, gwd, gbd = x.to(gpu_device), gw.to(gpu_device), gb.to(gpu_device)
-    got = K.route_and_dispatch(xd, gwd, gbd, k, 1.0)
+    counts_host = torch.full((E,), -1, dtype=torch.int32).pin_memory()
+    got = K.route_and_dispatch(xd, gwd, gbd, k, 1.0, counts_host=counts_host)
+    torch.cuda.synchronize()
+    assert torch.equal(counts_host, got[4].cpu())
     idx, idx64, w, v = K.router_fwd(xd, gwd, gbd, k, 1.0)
     ref = (idx, idx64, w, v) + tuple(K.dispatch(idx, xd, E))
     for a, b in zip(got, ref):
@@ -170,7 +176,10 @@ def test_route_and_dispatch_empty_batch(gpu_device):
     x = torch.empty(0, d, dtype=torch.bfloat16, device=gpu_device)
     gw = torch.randn(E, d, device=gpu_device).bfloat16()
     gb = torch.zeros(E, device=gpu_device).bfloat16()
-    out = K.route_and_dispatch(x, gw, gb, k, 1.0)
+    counts_host = torch.full((E,), -1, dtype=torch.int32).pin_memory()
+    out = K.route_and_dispatch(x, gw, gb, k, 1.0, counts_host=counts_host)
+    torch.cuda.synchronize()
+    assert counts_host.tolist() == [0] * E
     assert out[4].cpu().tolist() == [0] * E and out[5].cpu().tolist() == [0] * (E + 1)
     assert out[6].numel() == 0 and out[8].shape == (0, d)
 

@@ -86,11 +86,11 @@ def test_argument_errors_without_gpu():
                                    None, None, None, None) == 1
     # routing + dispatch of any batch: shape checks before any pointer is used, workspace size
     assert lib.fmoe_route_and_dispatch(None, None, None, 4, 4096, 8, 2, 1.0, None, None, None, None, None, None,
-                                       None, None, None, None, 0, None) == 2  # dim > 2048
+                                       None, None, None, None, None, 0, None) == 2  # dim > 2048
     assert lib.fmoe_route_and_dispatch(None, None, None, 4, 768, 65, 2, 1.0, None, None, None, None, None, None,
-                                       None, None, None, None, 0, None) == 7
+                                       None, None, None, None, None, 0, None) == 7
     assert lib.fmoe_route_and_dispatch(None, None, None, 4, 768, 8, 2, 1.0, None, None, None, None, None, None,
-                                       None, None, None, None, 0, None) == 1  # null outputs
+                                       None, None, None, None, None, 0, None) == 1  # null outputs
     assert lib.fmoe_route_and_dispatch_workspace_bytes(16384, 8, 2) == 2 * 512 * 8 * 4
     assert lib.fmoe_route_and_dispatch_workspace_bytes(33, 64, 6) == 2 * 2 * 64 * 4
     # size queries
