@@ -81,22 +81,37 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(
   const float w = weights[slot];
   const int chunks = dim / 8;
   float part = 0.0f;
-  for (int c = lane; c < chunks; c += 64) {
-    float g[8], of[8], d[8];
-    if (dy_dtype == FMOE_BF16) {
-      unpack8(reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(dy) + t * dim)[c], g);
-    } else {
-      const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(dy) + t * dim + c * 8);
-      const float4 a = p[0], b = p[1];
-      g[0] = a.x; g[1] = a.y; g[2] = a.z; g[3] = a.w; g[4] = b.x; g[5] = b.y; g[6] = b.z; g[7] = b.w;
-    }
-    unpack8(reinterpret_cast<const uint4*>(eo + r * dim)[c], of);
+  // two chunks per lane and pass (lane, lane + 64), both rows' loads issued
+  // before either is used; the sums keep the chunk order of the lane
+  for (int c0 = lane; c0 < chunks; c0 += 128) {
+    const int c1 = c0 + 64;
+    const bool has1 = c1 < chunks;
+    const int cc[2] = {c0, has1 ? c1 : c0};
+    float g[2][8], of[2][8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      d[i] = g[i] * w;
-      part = part + g[i] * of[i];
+    for (int q = 0; q < 2; ++q) {
+      const int c = cc[q];
+      if (dy_dtype == FMOE_BF16) {
+        unpack8(reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(dy) + t * dim)[c], g[q]);
+      } else {
+        const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(dy) + t * dim + c * 8);
+        const float4 a = p[0], b = p[1];
+        g[q][0] = a.x; g[q][1] = a.y; g[q][2] = a.z; g[q][3] = a.w;
+        g[q][4] = b.x; g[q][5] = b.y; g[q][6] = b.z; g[q][7] = b.w;
+      }
+      unpack8(reinterpret_cast<const uint4*>(eo + r * dim)[c], of[q]);
     }
-    reinterpret_cast<uint4*>(d_eo + r * dim)[c] = pack8(d);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      if (q == 1 && !has1) break;
+      float d[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        d[i] = g[q][i] * w;
+        part = part + g[q][i] * of[q][i];
+      }
+      reinterpret_cast<uint4*>(d_eo + r * dim)[cc[q]] = pack8(d);
+    }
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) part = part + __shfl_xor(part, off, 64);
