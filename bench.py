@@ -264,7 +264,7 @@ def cpu_info() -> dict:
 
 
 def cpu_c1_forward(runs=3):
-    """BASELINE.md's CPU baseline: workload C1, the reference forward
+    """The headline's CPU baseline: workload C1, the reference forward
     (models/moe.py:79-87, module semantics) in fp32 on the host cores at
     T = 16384 (x [8, 2048, 768] from N(0,1) seed 0, weights N(0, 0.02^2),
     zero bias); one warmup, then the median of `runs` timed forwards."""
@@ -297,7 +297,7 @@ def cpu_baseline(cfg, data, n_tokens, seconds=12.0):
     models/moe.py, bf16, forward + backward, on the first n_tokens tokens,
     repeated until about `seconds` of CPU work (at least 3 passes, at most
     2.5x that time); value = n_tokens / the median pass time.  Also runs
-    BASELINE.md's C1 fp32 forward (cpu_c1_forward) and names the host CPU."""
+    the C1 fp32 forward on the host cores (cpu_c1_forward) and names the host CPU."""
     from oracle import moe_oracle as mo
     threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count() or 1
     torch.set_num_threads(threads)
