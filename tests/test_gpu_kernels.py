@@ -417,10 +417,13 @@ def test_backward_products(gpu_device, counts, shared, d, I):
         assert rel_l2(dw3[grp].cpu(), dw3_ref) < 1e-5
 
 
-def _row_products(D, x_r, x_s, do_r, do_s, offsets, E, w1, w3, w2, w13t, w2t, ab_in, h_in, dab_in, split):
+def _row_products(D, x_r, x_s, do_r, do_s, offsets, E, w1, w3, w2, w13t, w2t, ab_in, h_in, dab_in, split,
+                  short_ws=False):
     """The four row products through the C ABI, with the split workspace or
-    without it; each product reads fixed inputs (not the previous product's
-    output), so only its own summation order differs between the two runs."""
+    without it (short_ws: a workspace one byte smaller than the query asks
+    for, which the products must treat as none); each product reads fixed
+    inputs (not the previous product's output), so only its own summation
+    order differs between the two runs."""
     from fusionllm_amd import _lib
     lib = _lib.load()
     rows_r, d = x_r.shape
@@ -430,6 +433,8 @@ def _row_products(D, x_r, x_s, do_r, do_s, offsets, E, w1, w3, w2, w13t, w2t, ab
     ws_bytes = lib.fmoe_split_workspace_bytes() if split else 0
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=D)
     wsp = ws.data_ptr() if split else None
+    if short_ws:
+        ws_bytes -= 1
     pa = lambda ts: _lib.ptr_array([t.data_ptr() for t in ts])
     st = K._stream()
     ab = torch.empty(rows, 2 * I, dtype=torch.bfloat16, device=D)
@@ -477,6 +482,10 @@ def test_split_tail_matches_whole_tiles(gpu_device):
     args = (D, x_r, x_s, do_r, do_s, offsets, E, w1, w3, w2, w13t, w2t, ab_in, h_in, dab_in)
     split = _row_products(*args, split=True)
     whole = _row_products(*args, split=False)
+    # a workspace smaller than the query runs every tile whole
+    short = _row_products(*args, split=True, short_ws=True)
+    for name, a, b in zip(("ab", "h", "out", "d_ab", "dx_rows"), short, whole):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), name
     names = ("ab", "h", "out", "d_ab", "dx_rows")
     for name, a, b in zip(names, split, whole):
         assert torch.equal(a[:counts[0]], b[:counts[0]]), name
