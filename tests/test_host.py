@@ -110,6 +110,17 @@ def test_argument_errors_without_gpu():
                                  None) == 2  # cols not a multiple of 4
 
 
+def test_host_counts_buffer_checks():
+    # the routing entry point writes the expert counts into host memory only
+    # through a contiguous pinned int32 buffer of at least E entries
+    from fusionllm_amd import _kernels as K
+    assert K._host_counts(None, 8) is None
+    with pytest.raises(RuntimeError, match="pinned"):
+        K._host_counts(torch.zeros(8, dtype=torch.int32), 8)  # pageable
+    with pytest.raises(RuntimeError, match="pinned"):
+        K._host_counts(torch.zeros(8, dtype=torch.int64), 8)  # also the wrong dtype
+
+
 def test_parameter_names_shapes_and_count():
     cfg = configs.C2.moe_config()
     m = DeepSeekMoE(cfg)
