@@ -421,6 +421,9 @@ def optimizer_bench(args):
                      "work_per_launch": work, "launches_timed": len(launches)},
         "cpu_baseline": cpu,
     }
+    c1 = (cpu or {}).get("c1_fp32_forward")
+    if c1 and c1.get("value") and not args.fwd_only:
+        line["vs_c1_fp32_forward"] = round(tok_s / c1["value"], 1)
     print(json.dumps(line), flush=True)
 
 
@@ -646,7 +649,10 @@ def main():
         "ms_per_step": round(elapsed / args.steps * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": None,
+        # the same-run CPU baseline of this metric (BASELINE.md publishes no
+        # number): the reference's module semantics on the box's host cores
+        "vs_baseline": (round(tok_s / cpu["value"], 1) if cpu and cpu.get("value") else None),
+        "vs_baseline_of": ("cpu_baseline.value: " + cpu["sample"]) if cpu and cpu.get("value") else None,
         "dtype": "bf16",
         "data": f"synthetic (seeded N(0,1) input, N(0,0.02^2) weights, router bias {cfg.bias})",
         "config": {"workload": cfg.name, "tokens": T, "dim": cfg.dim, "inter": cfg.inter,
@@ -661,6 +667,9 @@ def main():
         "kernels": kernels,
         "cpu_baseline": cpu,
     }
+    c1 = (cpu or {}).get("c1_fp32_forward")
+    if c1 and c1.get("value") and not args.fwd_only:
+        line["vs_c1_fp32_forward"] = round(tok_s / c1["value"], 1)
     print(json.dumps(line), flush=True)
 
 

@@ -123,11 +123,21 @@ def route_dispatch(x, gate_w, gate_b, k: int, route_scale: float):
 
 
 def _host_counts(counts_host, E):
+    """Address of the host buffer that receives the E expert counts (int32,
+    written by a kernel): a contiguous pinned int32 CPU tensor of at least E
+    elements, checked in that order (each failure names its reason)."""
     if counts_host is None:
         return None
-    if (counts_host.device.type != "cpu" or not counts_host.is_pinned() or counts_host.dtype != torch.int32
-            or counts_host.numel() < E or not counts_host.is_contiguous()):
-        raise RuntimeError("counts_host must be a contiguous pinned int32 CPU tensor of at least n_experts")
+    if counts_host.device.type != "cpu":
+        raise RuntimeError("counts_host must be a CPU tensor")
+    if counts_host.dtype != torch.int32:
+        raise RuntimeError(f"counts_host must be int32 (got {counts_host.dtype})")
+    if counts_host.numel() < E:
+        raise RuntimeError(f"counts_host must hold at least n_experts={E} elements (got {counts_host.numel()})")
+    if not counts_host.is_contiguous():
+        raise RuntimeError("counts_host must be contiguous")
+    if not counts_host.is_pinned():
+        raise RuntimeError("counts_host must be pinned host memory")
     return counts_host.data_ptr()
 
 
@@ -202,21 +212,46 @@ def gateup_fwd(x_perm, x_shared, offsets, n_experts: int, w1s, w3s, inter: int):
     rows = rows_r + rows_s
     ab = torch.empty(rows, 2 * inter, dtype=torch.bfloat16, device=dev)
     h = torch.empty(rows, inter, dtype=torch.bfloat16, device=dev)
-    ws, ws_bytes = _split_workspace(dev)
+    ws, ws_bytes = _split_workspace(dev, rows_r, rows_s, -(-inter // 128), small=True)
     check(lib.fmoe_gateup_fwd(_req(x_perm, "x_perm", torch.bfloat16),
                               _req(x_shared, "x", torch.bfloat16) if x_shared is not None else None,
                               _req(offsets, "offsets", torch.int32), n_experts, rows_r, rows_s, d, inter,
                               ptr_array([w.data_ptr() for w in w1s]), ptr_array([w.data_ptr() for w in w3s]),
-                              ab.data_ptr(), h.data_ptr(), ws.data_ptr(), ws_bytes, _stream()),
+                              ab.data_ptr(), h.data_ptr(), _ptr(ws), ws_bytes, _stream()),
           "fmoe_gateup_fwd")
     return ab, h
 
 
-def _split_workspace(dev):
-    """fp32 workspace for the K-split last round of the row products."""
+SMALL_LAUNCH_ROWS = 4096  # launches up to this many rows send groups of <= 128 rows to the small kernel
+SPLIT_MAX_ROUNDS = 8      # a row product of this many full rounds of tiles or more is never K-split
+
+
+@functools.lru_cache(maxsize=None)
+def _device_cus(index: int) -> int:
+    return torch.cuda.get_device_properties(index).multi_processor_count
+
+
+def _split_workspace(dev, rows_routed: int = 0, rows_shared: int = 0, tile_cols: int = 0, small: bool = False):
+    """fp32 workspace for the K-split last round of the row products, or
+    (None, 0) when the launch cannot split a tile (the library then runs
+    every tile whole): a decode-sized forward launch whose groups all go to
+    the small-group kernel (small: the product has one; at most 256 routed
+    and 128 shared rows in at most SMALL_LAUNCH_ROWS), or a product of
+    SPLIT_MAX_ROUNDS rounds or more (tile_cols: output tiles per 256-row
+    block)."""
+    if small and rows_routed <= 256 and rows_shared <= 128 and rows_routed + rows_shared <= SMALL_LAUNCH_ROWS:
+        return None, 0
+    if tile_cols:
+        blocks = -(-rows_routed // 256) + -(-rows_shared // 256)
+        if blocks * tile_cols >= SPLIT_MAX_ROUNDS * _device_cus(dev.index if dev.index is not None else 0):
+            return None, 0
     lib = _lib.load()
     nbytes = lib.fmoe_split_workspace_bytes()
     return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev), nbytes
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
 
 
 @_timed
@@ -224,10 +259,10 @@ def down_fwd(h, offsets, n_experts: int, rows_routed: int, rows_shared: int, w2s
     lib = _lib.load()
     rows, inter = h.shape
     out = torch.empty(rows, dim, dtype=torch.bfloat16, device=h.device)
-    ws, ws_bytes = _split_workspace(h.device)
+    ws, ws_bytes = _split_workspace(h.device, rows_routed, rows_shared, -(-dim // 256), small=True)
     check(lib.fmoe_down_fwd(_req(h, "h", torch.bfloat16), _req(offsets, "offsets", torch.int32), n_experts,
                             rows_routed, rows_shared, dim, inter, ptr_array([w.data_ptr() for w in w2s]),
-                            out.data_ptr(), ws.data_ptr(), ws_bytes, _stream()),
+                            out.data_ptr(), _ptr(ws), ws_bytes, _stream()),
           "fmoe_down_fwd")
     return out
 
@@ -291,12 +326,12 @@ def down_bwd_dx(d_out_routed, d_out_shared, offsets, n_experts: int, w2t, ab, in
     if tuple(w2t.shape) != (G, inter, d):
         raise RuntimeError(f"w2t must be {(G, inter, d)} (got {tuple(w2t.shape)})")
     d_ab = torch.empty(rows_r + rows_s, 2 * inter, dtype=torch.bfloat16, device=ab.device)
-    ws, ws_bytes = _split_workspace(ab.device)
+    ws, ws_bytes = _split_workspace(ab.device, rows_r, rows_s, -(-inter // 256))
     check(lib.fmoe_down_bwd_dx(_req(d_out_routed, "d_out", torch.bfloat16),
                                _req(d_out_shared, "d_out_shared", torch.bfloat16) if d_out_shared is not None else None,
                                _req(offsets, "offsets", torch.int32), n_experts, rows_r, rows_s, d, inter,
                                _req(w2t, "w2t", torch.bfloat16), _req(ab, "ab", torch.bfloat16),
-                               d_ab.data_ptr(), ws.data_ptr(), ws_bytes, _stream()),
+                               d_ab.data_ptr(), _ptr(ws), ws_bytes, _stream()),
           "fmoe_down_bwd_dx")
     return d_ab
 
@@ -309,11 +344,11 @@ def gateup_bwd_dx(d_ab, offsets, n_experts: int, rows_routed: int, rows_shared: 
     if tuple(w13t.shape) != (G, dim, two_i):
         raise RuntimeError(f"w13t must be {(G, dim, two_i)} (got {tuple(w13t.shape)})")
     dx_rows = torch.empty(rows, dim, dtype=torch.bfloat16, device=d_ab.device)
-    ws, ws_bytes = _split_workspace(d_ab.device)
+    ws, ws_bytes = _split_workspace(d_ab.device, rows_routed, rows_shared, -(-dim // 256))
     check(lib.fmoe_gateup_bwd_dx(_req(d_ab, "d_ab", torch.bfloat16), _req(offsets, "offsets", torch.int32),
                                  n_experts, rows_routed, rows_shared, dim, two_i // 2,
                                  _req(w13t, "w13t", torch.bfloat16), dx_rows.data_ptr(),
-                                 ws.data_ptr(), ws_bytes, _stream()),
+                                 _ptr(ws), ws_bytes, _stream()),
           "fmoe_gateup_bwd_dx")
     return dx_rows
 

@@ -316,6 +316,10 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
     P[p] = *reinterpret_cast<const bf16x8*>(smem + A_BYTES + (xb + 2048u * p));
 #pragma unroll
   for (int q = 0; q < 4; ++q) Q[0][q] = *reinterpret_cast<const bf16x8*>(smem + (xa + 2048u * q));
+  // Q[1] is a read-write operand of the first block8 statements (overwritten
+  // there by their ds_reads): give it a defined value.
+#pragma unroll
+  for (int q = 0; q < 4; ++q) Q[1][q] = Q[0][q];
 
   f32x4 acc[FM][FN];
 #pragma unroll

@@ -8,8 +8,8 @@
 // * Global -> LDS copies use global_load_lds_dwordx4 (16 bytes per lane written
 //   straight into LDS, no VGPR round trip).  One wave instruction writes 1 KB
 //   of LDS = 8 rows; the 16-byte chunks of a row are XOR-swizzled
-//   (slot = chunk ^ ((row ^ row >> 3) & 7)) by choosing which global chunk a lane
-//   fetches, which makes the fragment reads below free of bank conflicts.
+//   (slot = chunk ^ (row & 7), swzk below) by choosing which global chunk a
+//   lane fetches, which makes the fragment reads below free of bank conflicts.
 // * The copies and the LDS fragment reads are issued from inline assembly so
 //   that the compiler neither reorders them nor inserts conservative
 //   vmcnt(0) waits between the copies and the reads; every wait is explicit.
@@ -85,6 +85,11 @@ __device__ __forceinline__ void wait_vm_barrier() {
 // p = 0..1.  Reads next-step fragments: Q'[x] (A side) into nq, and P[2x],
 // P[2x+1] (B side) in place after their last use.  WAIT = lgkmcnt bound that
 // guarantees the fragments this block consumes have arrived.
+// The reads are still in flight when the statement ends: their destinations
+// are read-write operands ("+v"), so each keeps one register across the loop
+// that is consumed only by a later block8, after the s_waitcnt that covers
+// it (tests/test_host.py checks the built code for any other access to a
+// pending ds_read destination).
 template <int WAIT>
 __device__ __forceinline__ void block8(f32x4& c00, f32x4& c01, f32x4& c02, f32x4& c03, f32x4& c10, f32x4& c11,
                                        f32x4& c12, f32x4& c13, bf16x8& p0, bf16x8& p1, const bf16x8& q0,
@@ -100,7 +105,7 @@ __device__ __forceinline__ void block8(f32x4& c00, f32x4& c01, f32x4& c02, f32x4
       FMOE_MF("%[c12]", "%[p1]", "%[q2]") FMOE_MF("%[c13]", "%[p1]", "%[q3]")
       FMOE_DS("%[p1]", "%[ap1]")
       : [c00] "+v"(c00), [c01] "+v"(c01), [c02] "+v"(c02), [c03] "+v"(c03), [c10] "+v"(c10), [c11] "+v"(c11),
-        [c12] "+v"(c12), [c13] "+v"(c13), [p0] "+v"(p0), [p1] "+v"(p1), [nq] "=&v"(nq)
+        [c12] "+v"(c12), [c13] "+v"(c13), [p0] "+v"(p0), [p1] "+v"(p1), [nq] "+v"(nq)
       : [q0] "v"(q0), [q1] "v"(q1), [q2] "v"(q2), [q3] "v"(q3), [aq] "v"(aq), [ap0] "v"(ap0), [ap1] "v"(ap1),
         [wt] "n"(WAIT));
 }

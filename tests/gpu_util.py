@@ -38,7 +38,7 @@ def bf16_ulp(t: torch.Tensor) -> torch.Tensor:
 
 
 
-def close_block_output(y, y_ref, y_truth, terms_fn, k, rtol, atol, max_frac=1e-5):
+def close_block_output(y, y_ref, y_truth, terms_fn, k, rtol, atol, max_frac=1e-5, label=""):
     """The block output against the reference's bf16 composition y_ref:
     within rtol/atol elementwise, except where the terms of an output element
     cancel.  The reference rounds each expert's output and its weighted copy,
@@ -51,12 +51,17 @@ def close_block_output(y, y_ref, y_truth, terms_fn, k, rtol, atol, max_frac=1e-5
     largest term (k weighted expert outputs, the routed sum, the shared
     output, the sum: half an ulp each).  terms_fn(rows) returns, for those
     token rows, the fp32 terms [rows, k + 1, d]: the k weighted expert
-    outputs and the shared output."""
+    outputs and the shared output.  Prints and returns the number of
+    elements that needed that bound."""
     a, b, t = y.double().cpu(), y_ref.double().cpu(), y_truth.double().cpu()
     err = (a - b).abs()
     bad = err > atol + rtol * b.abs()
+    n_bad = int(bad.sum())
+    # how many elements needed the cancellation bound (reported for every call)
+    print(f"[close_block_output] {label}: {n_bad} of {bad.numel()} elements outside rtol {rtol} / atol {atol} "
+          f"of the bf16 reference ({n_bad / max(bad.numel(), 1):.2e}; limit {max_frac:.0e})", flush=True)
     if not bad.any():
-        return
+        return 0
     assert float(bad.double().mean()) <= max_frac, (f"{int(bad.sum())}/{bad.numel()} elements out of tolerance "
                                                     f"(rtol={rtol}, atol={atol}); max abs err {float(err.max()):.3e}")
     rows = bad.any(-1).nonzero().flatten()
@@ -69,3 +74,4 @@ def close_block_output(y, y_ref, y_truth, terms_fn, k, rtol, atol, max_frac=1e-5
               for i in range(min(4, int(over.sum())))]
     assert not over.any(), (f"{int(over.sum())} of {int(bad.sum())} elements out of tolerance exceed the rounding "
                             f"bound of the composition; (gpu, ref, truth, largest term): {detail}")
+    return n_bad

@@ -27,7 +27,7 @@ from fusionllm_amd import _kernels as K
 from fusionllm_amd import configs, moe_residual
 from oracle import moe_oracle as mo
 from tests.gpu_util import build_module, close_block_output, f32_bits, rel_l2
-from tests.test_gpu_moe import W_REL_L2, Y_TOL, _check_dx, _gpu_run, _oracle_run, _routing_exact
+from tests.test_gpu_moe import DX_ATOL_PER_TERM, DX_RTOL, W_REL_L2, Y_TOL, _check_dx, _gpu_run, _oracle_run, _routing_exact
 
 pytestmark = pytest.mark.gpu
 
@@ -94,7 +94,11 @@ def test_full_c2_forward_backward_against_oracle(gpu_device):
     _routing_exact(data, g, cfg)
     o = _oracle_run(cfg, data, g["idx"])
     truth = _oracle_run(cfg, data, g["idx"], dtype=torch.float32)
-    close_block_output(g["y"], o["y"], truth["y"], _terms(cfg, data, g["idx"]), cfg.topk, **Y_TOL)
+    n_esc = close_block_output(g["y"], o["y"], truth["y"], _terms(cfg, data, g["idx"]), cfg.topk, label="C2",
+                               **Y_TOL)
+    # (the printed count is recorded in the design notes; the bound leaves
+    # room for last-bit differences of a changed GEMM summation order)
+    assert n_esc <= 40, f"C2: {n_esc} elements needed the cancellation bound"
     _check_grads(g, o)
     _check_dx(g["dx"], o["dx"], truth["dx"], cfg.topk)
 
@@ -111,18 +115,29 @@ def test_full_c5_forward_backward_against_oracle(gpu_device):
     _routing_exact(data, g, cfg)
     o = _oracle_run(cfg, data, g["idx"])
     truth = _oracle_run(cfg, data, g["idx"], dtype=torch.float32)
-    close_block_output(g["y"], o["y"], truth["y"], _terms(cfg, data, g["idx"]), cfg.topk, **Y_TOL)
+    n_esc = close_block_output(g["y"], o["y"], truth["y"], _terms(cfg, data, g["idx"]), cfg.topk, label="C5",
+                               **Y_TOL)
+    assert n_esc <= 200, f"C5: {n_esc} elements needed the cancellation bound"
     _check_grads(g, o)
     _check_dx(g["dx"], o["dx"], truth["dx"], cfg.topk)
 
 
-def test_full_c4_stack_routing_and_output(gpu_device):
-    # C4 at its full size: 16 x (RMSNorm + MoE + residual) on [4, 4096, 768].
-    # Routing bit-exact in all 16 layers (against the C router on that layer's
-    # GPU input); the stack's output against the reference run layer by layer
-    # on the GPU's routing (relative L2 to the fp32-arithmetic truth <= 1e-2
-    # and within 1.5x the bf16 reference's own, as at 1024 tokens); forward
-    # and backward run, the gradients finite.
+@pytest.mark.timeout(900)
+def test_full_c4_stack_forward_backward_against_oracle(gpu_device):
+    # C4 at its full size: 16 x (RMSNorm + MoE + residual) on [4, 4096, 768]
+    # (models/fusionllm.py:50-53), forward and backward.  Routing bit-exact in
+    # all 16 layers (against the C router on that layer's GPU input); the
+    # stack is then run on the host layer by layer on the GPU's routing, in
+    # bf16 (the reference's composition) and in fp32 arithmetic on the same
+    # bf16 operands (the truth), both with autograd:
+    # * output and dx: relative L2 to the truth <= 1e-2 and within 1.5x the
+    #   bf16 reference's own; dx elementwise within the single-block bound
+    #   (tests/test_gpu_moe.py _check_dx: |dx_ref - t| + (k+2) * 2.5e-3 +
+    #   2e-2 |t|, here with k+3 terms for the norm) summed over the 16 layers,
+    #   the worst case of independent per-layer rounding;
+    # * every parameter gradient of the first, middle and last layers
+    #   (experts, gate, shared expert, norm weight) within relative L2 1e-2 of
+    #   the bf16 reference's.
     cfg = configs.C4
     L, T, eps = cfg.layers, cfg.tokens, 1e-6
     layers = [configs.make_block(cfg, seed=100 + l, with_dy=False) for l in range(L)]
@@ -140,32 +155,70 @@ def test_full_c4_stack_routing_and_output(gpu_device):
         routing.append(m._last_indices.cpu())
     h.backward(dy.to(gpu_device, torch.bfloat16).view(*cfg.x_shape))
     out_gpu = h.detach().reshape(T, cfg.dim).cpu()
-    assert torch.isfinite(x.grad).all()
-    assert all(torch.isfinite(p.grad).all() for m in mods for p in m.parameters() if p.grad is not None)
+    dx_gpu = x.grad.reshape(T, cfg.dim).cpu()
+    check_layers = (0, L // 2, L - 1)
+    grads_gpu = {}
+    for l in check_layers:
+        gl = {name: (None if p.grad is None else p.grad.cpu()) for name, p in mods[l].named_parameters()}
+        gl["norm.weight"] = norms[l].weight.grad.cpu()
+        grads_gpu[l] = gl
     ones = torch.ones(cfg.dim, dtype=torch.bfloat16)
     for l in range(L):
         xn, _ = K.rmsnorm_fwd(ins[l].contiguous(), ones.to(gpu_device), eps)
         ridx, _, _ = mo.router_c(xn.cpu(), layers[l].gate_w.bfloat16(), layers[l].gate_b.bfloat16(),
                                  cfg.topk, cfg.route_scale)
         assert torch.equal(routing[l], ridx.long()), f"layer {l}"
-    del mods, norms, h, ins
+    del mods, norms, h, ins, x
+    torch.cuda.empty_cache()
 
-    @torch.no_grad()
     def oracle_stack(dtype):
-        hh = x0.bfloat16().to(dtype)
+        xo = x0.bfloat16().to(dtype).clone().requires_grad_(True)
+        hh, params = xo, {}
         for l in range(L):
-            sd = {k: v.bfloat16().to(dtype) for k, v in layers[l].state_dict().items()}
+            sd = {k: v.bfloat16().to(dtype).clone().requires_grad_(l in check_layers)
+                  for k, v in layers[l].state_dict().items()}
+            nw = ones.to(dtype).clone().requires_grad_(l in check_layers)
+            if l in check_layers:
+                params[l] = (sd, nw)
             experts = [(sd[f"experts.{e}.w1.weight"], sd[f"experts.{e}.w3.weight"],
                         sd[f"experts.{e}.w2.weight"]) for e in range(cfg.n_experts)]
             shared = (sd["shared_expert.w1.weight"], sd["shared_expert.w3.weight"], sd["shared_expert.w2.weight"])
-            xn = mo.rms_norm(hh, ones.to(dtype), eps)
+            xn = mo.rms_norm(hh, nw, eps)
             w, idx = mo.route(xn, sd["gate.weight"], sd["gate.bias"], cfg.topk, 1.0, mode="fp32",
                               indices=routing[l])
-            y, _, _ = mo.moe_forward(xn, None, None, experts, shared, cfg.topk, 1.0, routing=(w, idx))
+            y, _, _ = mo.moe_forward(xn, sd["gate.weight"], sd["gate.bias"], experts, shared, cfg.topk, 1.0,
+                                     routing=(w, idx))
             hh = hh + y
-        return hh
+        hh.backward(dy.bfloat16().to(dtype))
+        grads = {}
+        for l, (sd, nw) in params.items():
+            gl = {name: t.grad for name, t in sd.items()}
+            gl["norm.weight"] = nw.grad
+            grads[l] = gl
+        return hh.detach(), xo.grad, grads
 
-    out_ref, out_t = oracle_stack(torch.bfloat16), oracle_stack(torch.float32)
-    e_gpu, e_ref = rel_l2(out_gpu, out_t), rel_l2(out_ref, out_t)
-    assert e_gpu <= 1e-2, f"out: relative L2 to the truth {e_gpu:.3e}"
-    assert e_gpu <= 1.5 * e_ref + 1e-4, f"out: rel L2 {e_gpu:.3e} vs the bf16 reference's {e_ref:.3e}"
+    out_ref, dx_ref, g_ref = oracle_stack(torch.bfloat16)
+    out_t, dx_t, _ = oracle_stack(torch.float32)
+    for got, ref, t, what in ((out_gpu, out_ref, out_t, "out"), (dx_gpu, dx_ref, dx_t, "dx")):
+        e_gpu, e_ref = rel_l2(got, t), rel_l2(ref, t)
+        print(f"[c4-full] {what}: rel L2 to truth {e_gpu:.3e} (bf16 reference {e_ref:.3e})", flush=True)
+        assert e_gpu <= 1e-2, f"{what}: relative L2 to the truth {e_gpu:.3e}"
+        assert e_gpu <= 1.5 * e_ref + 1e-4, f"{what}: rel L2 {e_gpu:.3e} vs the bf16 reference's {e_ref:.3e}"
+    a, r, t = dx_gpu.double(), dx_ref.double(), dx_t.double()
+    slack = L * (cfg.topk + 3) * DX_ATOL_PER_TERM + DX_RTOL * t.abs()
+    err = (a - t).abs()
+    ratio = float(((err - (r - t).abs()).clamp_min(0) / slack).max())
+    print(f"[c4-full] dx: max |dx - t| {float(err.max()):.3e}, max |dx_ref - t| {float((r - t).abs().max()):.3e}, "
+          f"largest share of the element bound used {ratio:.3f}", flush=True)
+    assert ratio <= 1.0, f"dx: an element exceeds |dx_ref - t| + the summed per-layer bound ({ratio:.3f})"
+    for l in check_layers:
+        for name, ref in g_ref[l].items():
+            got = grads_gpu[l][name]
+            assert (got is None) == (ref is None), (l, name)
+            if ref is None:
+                continue
+            err = rel_l2(got, ref)
+            assert err <= W_REL_L2, f"layer {l} {name}: relative L2 to the bf16 reference {err:.3e}"
+        worst = max(rel_l2(grads_gpu[l][n], g) for n, g in g_ref[l].items() if g is not None)
+        print(f"[c4-full] layer {l}: largest parameter-gradient rel L2 to the bf16 reference {worst:.3e}",
+              flush=True)

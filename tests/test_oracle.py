@@ -133,6 +133,38 @@ def test_router_differs_from_bf16_module_router_only_at_bf16_near_ties(cfg):
     assert torch.equal(torch.sort(i64, -1).values, torch.sort(idx.long(), -1).values)
 
 
+@pytest.mark.parametrize("cfg", [configs.C2, configs.C5], ids=lambda c: c.name)
+def test_fp32_module_routing_differs_only_within_bf16_operand_rounding(cfg):
+    # Decision D19: an fp32 module outside autocast computes on bf16 copies of
+    # its operands (fmoe_cast_bf16), so it routes on fp32 logits of the
+    # bf16-rounded x, gate weight and bias (the C router, which the GPU
+    # matches bit for bit), while the reference's fp32 module routes on the
+    # fp32 operands themselves (models/moe.py:46-48).  The expert sets differ
+    # only where the fp64 scores of the k-th and (k+1)-th expert lie within
+    # what rounding the operands moves them: each product x_i W_ei changes by
+    # at most 2^-8 |x_i W_ei|, the bias by 2^-9 |b_e|, a score by at most 1/4
+    # of its logit's change (measured at full size, seed 0: C2 24 of 16384
+    # tokens (0.15 %) get a different set, 70 a different order; C5 452 of
+    # 32768 (1.4 %), 1670).
+    T = 4096 if cfg.n_experts == 64 else cfg.tokens
+    data = configs.make_block(cfg, seed=0, tokens=T, experts=False, with_dy=False)
+    x, gw, gb = data.x.float(), data.gate_w.float(), data.gate_b.float()
+    idx, _, _ = mo.router_c(x.bfloat16(), gw.bfloat16(), gb.bfloat16(), cfg.topk, cfg.route_scale)
+    _, im = mo.route(x, gw, gb, cfg.topk, cfg.route_scale, mode="module")
+    k = cfg.topk
+    logits = F.linear(x.double(), gw.double(), gb.double())
+    srt = torch.sort(torch.sigmoid(logits), dim=-1, descending=True).values
+    gap = srt[:, k - 1] - srt[:, k]
+    delta = 2.0 ** -8 * (x.double().abs() @ gw.double().abs().T) + 2.0 ** -9 * gb.double().abs()
+    bound = 2 * 0.25 * delta.max(-1).values * 1.01
+    differ = (torch.sort(idx.long(), -1).values != torch.sort(im, -1).values).any(-1)
+    assert differ.any()
+    assert float(differ.double().mean()) < 0.02
+    assert bool((gap[differ] <= bound[differ]).all()), "a set difference that operand rounding does not explain"
+    # a planted mistake fails: the bound with the bias term alone is too small
+    assert not bool((gap[differ] <= (0.5 * 2.0 ** -9 * gb.double().abs().max())).all())
+
+
 def test_router_normalisation_closed_form():
     x, gw, gb = _bf16_block(T=256, d=768, E=8)
     for rs in (1.0, 2.5):
