@@ -16,7 +16,7 @@ The JSON line also carries:
   kernels       the same figures for every entry point of the step: the
                 GEMMs from a short untimed pass with events around every
                 entry point (it also names the dominant one), the
-                HBM-bound routing, dispatch, combine, transpose and reduce
+                HBM-bound routing, dispatch, combine and reduce
                 entry points from graphs of 20 back-to-back launches (events
                 around such short kernels add their launch gaps);
   cpu_baseline  the reference algorithm (torch-CPU restatement, the oracle)
@@ -123,7 +123,6 @@ def kernel_model(cfg, T, active_groups=None):
         # reads the k routed + shared rows, x and d_out and writes dx
         "rmsnorm_fwd": ("hbm", T * (2 * d + 2 * d + 4)),
         "dx_reduce_norm": ("hbm", T * (k * 2 * d + 2 * d + 2 * d + 2 * d + 2 * d + 12 * k + 4)),
-        "transpose_weights": ("hbm", (E + (1 if cfg.n_shared else 0)) * 3 * d * I * 2 * 2),
     }
 
 
@@ -191,7 +190,7 @@ def graph_time(fn, reps=20, replays=20):
 def graph_hbm_times(m, x, dy):
     """Per-launch time (us) of the HBM-bound entry points of one forward +
     backward of the DeepSeekMoE block (routing, dispatch, combine and their
-    backward, the transposed weight copies), each from a graph of
+    backward), each from a graph of
     back-to-back launches on the workload's own intermediates (graph_time).
     Events around every call of an eager step inflate such short kernels by
     their launch gaps; this is the figure the roofline fractions of these
@@ -206,8 +205,6 @@ def graph_hbm_times(m, x, dy):
         fw = _forward_pass(meta, x, m.gate.weight, m.gate.bias, m._flat_weights())
         xb, gwb, wb, idx, idx64, w, v, counts, offsets, perm, pos, x_perm, ab, h, o, y = fw
         T, d = xb.shape
-        G = E + (1 if has_shared else 0)
-        w1s, w3s, w2s = wb[0::3][:G], wb[1::3][:G], wb[2::3][:G]
         gbb = m.gate.bias.to(torch.bfloat16).contiguous()
         dyb = dy.to(torch.bfloat16).contiguous()
         d_o, d_w = K.combine_bwd(dyb, o, w, perm, k)
@@ -221,7 +218,6 @@ def graph_hbm_times(m, x, dy):
             "router_bwd": lambda: K.router_bwd(d_w, v, perm, offsets, x_perm, E, rs, m.gate.weight.dtype),
             "route_and_dispatch": lambda: K.route_and_dispatch(xb, gwb, gbb, k, rs),
             "dx_reduce": lambda: K.dx_reduce(dx_rows, pos, idx, d_logits, gwb, T * k, has_shared, x.dtype),
-            "transpose_weights": lambda: K.transpose_weights(w1s, w3s, w2s),
         }
         return {name: graph_time(fn) for name, fn in calls.items()}
 

@@ -296,59 +296,49 @@ def combine_bwd(dy, expert_out, weights, perm, k: int):
     return d_eo, d_w
 
 
-@_timed
-def transpose_weights(w1s, w3s, w2s):
-    """Transposed weight copies for the dX products: (w13t [G, dim, 2I], w2t [G, I, dim])."""
-    lib = _lib.load()
-    G = len(w1s)
-    inter, dim = w1s[0].shape
-    dev = w1s[0].device
-    w13t = torch.empty(G, dim, 2 * inter, dtype=torch.bfloat16, device=dev)
-    w2t = torch.empty(G, inter, dim, dtype=torch.bfloat16, device=dev)
-    for name, ws, shape in (("w1", w1s, (inter, dim)), ("w3", w3s, (inter, dim)), ("w2", w2s, (dim, inter))):
-        for w in ws:
-            _req(w, name, torch.bfloat16)
-            if tuple(w.shape) != shape:
-                raise RuntimeError(f"{name} must be {shape} (got {tuple(w.shape)})")
-    check(lib.fmoe_transpose_weights(ptr_array([w.data_ptr() for w in w1s]), ptr_array([w.data_ptr() for w in w3s]),
-                                     ptr_array([w.data_ptr() for w in w2s]), G, dim, inter,
-                                     w13t.data_ptr(), w2t.data_ptr(), _stream()),
-          "fmoe_transpose_weights")
-    return w13t, w2t
+def _weights(ws, name, shape):
+    for w in ws:
+        _req(w, name, torch.bfloat16)
+        if tuple(w.shape) != shape:
+            raise RuntimeError(f"{name} must be {shape} (got {tuple(w.shape)})")
+    return ptr_array([w.data_ptr() for w in ws])
 
 
 @_timed
-def down_bwd_dx(d_out_routed, d_out_shared, offsets, n_experts: int, w2t, ab, inter: int):
+def down_bwd_dx(d_out_routed, d_out_shared, offsets, n_experts: int, w2s, ab, inter: int):
+    """dh = d_out w2 with the SwiGLU backward fused; w2s: per group [dim, inter] as nn.Linear keeps it."""
     lib = _lib.load()
     rows_r, d = d_out_routed.shape
     rows_s = d_out_shared.shape[0] if d_out_shared is not None else 0
     G = n_experts + (1 if rows_s else 0)
-    if tuple(w2t.shape) != (G, inter, d):
-        raise RuntimeError(f"w2t must be {(G, inter, d)} (got {tuple(w2t.shape)})")
+    if len(w2s) < G:
+        raise RuntimeError(f"down_bwd_dx needs {G} weight matrices (got {len(w2s)})")
     d_ab = torch.empty(rows_r + rows_s, 2 * inter, dtype=torch.bfloat16, device=ab.device)
     ws, ws_bytes = _split_workspace(ab.device, rows_r, rows_s, -(-inter // 256))
     check(lib.fmoe_down_bwd_dx(_req(d_out_routed, "d_out", torch.bfloat16),
                                _req(d_out_shared, "d_out_shared", torch.bfloat16) if d_out_shared is not None else None,
                                _req(offsets, "offsets", torch.int32), n_experts, rows_r, rows_s, d, inter,
-                               _req(w2t, "w2t", torch.bfloat16), _req(ab, "ab", torch.bfloat16),
+                               _weights(w2s[:G], "w2", (d, inter)), _req(ab, "ab", torch.bfloat16),
                                d_ab.data_ptr(), _ptr(ws), ws_bytes, _stream()),
           "fmoe_down_bwd_dx")
     return d_ab
 
 
 @_timed
-def gateup_bwd_dx(d_ab, offsets, n_experts: int, rows_routed: int, rows_shared: int, w13t, dim: int):
+def gateup_bwd_dx(d_ab, offsets, n_experts: int, rows_routed: int, rows_shared: int, w1s, w3s, dim: int):
+    """dx_rows = da w1 + db w3; w1s, w3s: per group [inter, dim] as nn.Linear keeps them."""
     lib = _lib.load()
     rows, two_i = d_ab.shape
+    inter = two_i // 2
     G = n_experts + (1 if rows_shared else 0)
-    if tuple(w13t.shape) != (G, dim, two_i):
-        raise RuntimeError(f"w13t must be {(G, dim, two_i)} (got {tuple(w13t.shape)})")
+    if len(w1s) < G or len(w3s) < G:
+        raise RuntimeError(f"gateup_bwd_dx needs {G} weight matrices of each kind")
     dx_rows = torch.empty(rows, dim, dtype=torch.bfloat16, device=d_ab.device)
     ws, ws_bytes = _split_workspace(d_ab.device, rows_routed, rows_shared, -(-dim // 256))
     check(lib.fmoe_gateup_bwd_dx(_req(d_ab, "d_ab", torch.bfloat16), _req(offsets, "offsets", torch.int32),
-                                 n_experts, rows_routed, rows_shared, dim, two_i // 2,
-                                 _req(w13t, "w13t", torch.bfloat16), dx_rows.data_ptr(),
-                                 _ptr(ws), ws_bytes, _stream()),
+                                 n_experts, rows_routed, rows_shared, dim, inter,
+                                 _weights(w1s[:G], "w1", (inter, dim)), _weights(w3s[:G], "w3", (inter, dim)),
+                                 dx_rows.data_ptr(), _ptr(ws), ws_bytes, _stream()),
           "fmoe_gateup_bwd_dx")
     return dx_rows
 

@@ -13,7 +13,7 @@ from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int64, c_size_
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libfusionmoe.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 MAX_EXPERTS = 64
 MAX_TOPK = 8
 
@@ -46,11 +46,10 @@ SIGNATURES = {
                                  c_int, c_int, _P, _P, _P]),
     "fmoe_combine_bwd": (c_int, [_P, c_int, _P, _P, _P, c_int64, c_int64, c_int,
                                  _P, _P, _P]),
-    "fmoe_transpose_weights": (c_int, [_PP, _PP, _PP, c_int, c_int64, c_int64, _P, _P, _P]),
     "fmoe_down_bwd_dx": (c_int, [_P, _P, _P, c_int, c_int64, c_int64, c_int64, c_int64,
-                                 _P, _P, _P, _P, c_size_t, _P]),
+                                 _PP, _P, _P, _P, c_size_t, _P]),
     "fmoe_gateup_bwd_dx": (c_int, [_P, _P, c_int, c_int64, c_int64, c_int64, c_int64,
-                                   _P, _P, _P, c_size_t, _P]),
+                                   _PP, _PP, _P, _P, c_size_t, _P]),
     "fmoe_weight_grad_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int, c_int64, c_int64]),
     "fmoe_weight_grad": (c_int, [_P, _P, c_int64, _P, _P, c_int64, _P, c_int,
                                  c_int64, c_int64, c_int64, c_int64, c_int64,

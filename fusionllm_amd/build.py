@@ -36,9 +36,13 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-source flags (none at present).
+EXTRA_FLAGS: dict[str, list[str]] = {}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}\n{res.stderr}")

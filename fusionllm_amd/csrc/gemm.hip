@@ -36,11 +36,12 @@
 namespace fmoe {
 
 // ---- row-grouped products ---------------------------------------------------
-// Every row-grouped product streams both operands K-contiguous: the
-// activations are row-major [rows, K]; the weights are nn.Linear weights
-// ([out, in], K = in) for the forward products and the transposed copies made
-// by fmoe_transpose_weights for the backward ones (w2t for dh = d_out * w2,
-// w13t for dx = [da | db] * [w1; w3]).
+// The activations are row-major [rows, K] (K-contiguous).  The weights are
+// the nn.Linear weights as they lie: [out, in] with K = in for the forward
+// products (K-contiguous, read like the activations), and [K, N] row-major
+// for the backward dX products (dh = d_out * w2 reads w2 [dim, inter];
+// dx = [da | db] * [w1; w3] reads w1, w3 [inter, dim]), whose B stages are
+// copied as they lie and read with transposing LDS reads (gemm_core.h).
 enum GemmMode { GATEUP_FWD = 0, DOWN_FWD = 1, DOWN_BWD = 2, GATEUP_BWD = 3 };
 
 struct GemmArgs {
@@ -54,13 +55,13 @@ struct GemmArgs {
   int K;        // reduction length
   int N;        // output columns (GATEUP_FWD: inter = h columns)
   int inter;    // SwiGLU width (GATEUP_FWD, DOWN_BWD)
-  int64_t ldb;  // leading dimension of the (K-contiguous) weight operand
+  int64_t ldb;  // leading dimension of the weight operand (row length as it lies in memory)
   uint16_t* c0;  // main output (ab / out / d_ab / dx_rows)
   uint16_t* c1;  // GATEUP_FWD: h
   const uint16_t* aux;  // DOWN_BWD: ab
   int64_t ldc0, ldc1, ldaux;
-  const uint16_t* b0[FMOE_MAX_EXPERTS + 1];  // w1 / w2 / w2t / w13t
-  const uint16_t* b1[FMOE_MAX_EXPERTS + 1];  // w3 (GATEUP_FWD only)
+  const uint16_t* b0[FMOE_MAX_EXPERTS + 1];  // w1 (GATEUP_*) / w2 (DOWN_*)
+  const uint16_t* b1[FMOE_MAX_EXPERTS + 1];  // w3 (GATEUP_*)
   int small_max;  // groups with 1 .. small_max rows go to small_gemm_kernel (0: none)
   int small_compact;  // DOWN_FWD small kernel: the grid covers only groups with rows
   float* split_ws;  // fp32 partials of the K-split tiles of the last round (nullptr: no split)
@@ -222,6 +223,9 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
 
   // GATEUP_FWD: a tile covers 128 h columns (128 rows of w1 and of w3).
   constexpr int TN_COLS = (MODE == GATEUP_FWD) ? BN / 2 : BN;
+  // The backward dX products read the weights as they lie ([K, N]) with
+  // transposing LDS reads.
+  constexpr bool BTR = (MODE == DOWN_BWD || MODE == GATEUP_BWD);
   const int tiles_n = (args.N + TN_COLS - 1) / TN_COLS;
   const int total_tiles = count_tiles(args, offsets, tiles_n);
   const int NP = static_cast<int>(gridDim.x), b = xcd_slot(static_cast<int>(blockIdx.x), NP);
@@ -257,6 +261,9 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
   // lane l fetches row 64 i + drow, global chunk dchunk (the swizzled slot l % 8).
   const int drow = w * 8 + (lane >> 3);
   const int dchunk = (lane & 7) ^ swzk(drow);  // swzk(64 i + drow) == swzk(drow)
+  // B as it lies (BTR): k row 16 i + drow_b, chunk cb_t (wsw(16 i + drow_b) == wsw(drow_b))
+  const int drow_b = 2 * w + (lane >> 5);
+  const int cb_t = ((((lane & 31) >> 1) ^ wsw(drow_b)) << 1) | (lane & 1);
   const uint32_t lds_copy = sbase + w * 1024;
   int c_ti = 0, c_kt = 0, c_k0 = 0, c_kn = 0;  // item ordinal, step within it, its K range
   const uint16_t* c_a = nullptr;   // A rows of the tile being copied
@@ -286,12 +293,25 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
       const int r = min(64 * i + drow, c_last_row);
       copy16(st + i * 8192, c_a + kofs, static_cast<uint32_t>(r * lda + dchunk * 8) * 2u);
     }
+    if constexpr (BTR) {
+      // 64 k rows of 512 bytes: instruction i of wave w writes k rows 16 i + 2 w, +1;
+      // lane l: k row 16 i + drow_b, logical 16-byte chunk cb_t (32-byte windows
+      // swizzled by wsw(k row)).  GATEUP_BWD: k < inter from w1, else from w3.
+      const uint16_t* bb = (MODE == GATEUP_BWD && kofs >= args.inter)
+                               ? c_b1 + static_cast<int64_t>(kofs - args.inter) * args.ldb
+                               : c_b0 + static_cast<int64_t>(kofs) * args.ldb;
+      const int col = min(c_n0 + 8 * cb_t, args.N - 8);
 #pragma unroll
-    for (int i = 0; i < LB; ++i) {
-      // GATEUP_FWD bands: w1 rows (even i) and w3 rows (odd i), 64 h columns each
-      const int n = min(c_n0 + ((MODE == GATEUP_FWD) ? (i >> 1) * 64 : 64 * i) + drow, args.N - 1);
-      const uint16_t* b = (MODE == GATEUP_FWD && (i & 1)) ? c_b1 : c_b0;
-      copy16(st + A_BYTES + i * 8192, b + kofs, static_cast<uint32_t>(n * ldb + dchunk * 8) * 2u);
+      for (int i = 0; i < LB; ++i)
+        copy16(st + A_BYTES + i * 8192, bb, static_cast<uint32_t>((16 * i + drow_b) * ldb + col) * 2u);
+    } else {
+#pragma unroll
+      for (int i = 0; i < LB; ++i) {
+        // GATEUP_FWD bands: w1 rows (even i) and w3 rows (odd i), 64 h columns each
+        const int n = min(c_n0 + ((MODE == GATEUP_FWD) ? (i >> 1) * 64 : 64 * i) + drow, args.N - 1);
+        const uint16_t* b = (MODE == GATEUP_FWD && (i & 1)) ? c_b1 : c_b0;
+        copy16(st + A_BYTES + i * 8192, b + kofs, static_cast<uint32_t>(n * ldb + dchunk * 8) * 2u);
+      }
     }
     if (++c_kt == c_kn) {
       c_kt = 0;
@@ -299,9 +319,9 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
     }
   };
 
-  // ---- fragment address bases (A rows / B rows of this wave)
+  // ---- fragment address bases (A rows / B rows of this wave; BTR: trb_base)
   uint32_t xa = frag_base(wm * WTM, lane);
-  uint32_t xb = frag_base(wn * WTN, lane);
+  uint32_t xb = BTR ? trb_base(wn, lane) : frag_base(wn * WTN, lane);
 
   issue(0);
   if (total > 1) {
@@ -313,7 +333,8 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
   bf16x8 P[FN], Q[2][4];
 #pragma unroll
   for (int p = 0; p < FN; ++p)
-    P[p] = *reinterpret_cast<const bf16x8*>(smem + A_BYTES + (xb + 2048u * p));
+    P[p] = BTR ? trb_frag(sbase + (xb ^ (static_cast<uint32_t>(p) << 5)))
+               : *reinterpret_cast<const bf16x8*>(smem + A_BYTES + (xb + 2048u * p));
 #pragma unroll
   for (int q = 0; q < 4; ++q) Q[0][q] = *reinterpret_cast<const bf16x8*>(smem + (xa + 2048u * q));
   // Q[1] is a read-write operand of the first block8 statements (overwritten
@@ -339,7 +360,10 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
     // keep the per-step fragment addresses from being hoisted out of the loop
     asm volatile("" : "+v"(xa), "+v"(xb));
     const uint32_t cur = sbase + (it & 1) * STAGE;
-    kstep<64>(acc, P, Q[0], Q[1], xa, xb, cur);  // reads the second K half of this stage
+    if constexpr (BTR)
+      kstep_t<1>(acc, P, Q[0], Q[1], xa, xb, cur);
+    else
+      kstep<64>(acc, P, Q[0], Q[1], xa, xb, cur);  // reads the second K half of this stage
     uint32_t src = cur;                           // the last step re-reads (harmlessly) its own stage
     if (it + 1 < total) {
       // Stage (it+1) must have landed; stage it&1 is free once every wave is past
@@ -352,7 +376,10 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
       if (it + 2 < total) issue(it + 2);
       src = sbase + ((it + 1) & 1) * STAGE;
     }
-    kstep<0>(acc, P, Q[1], Q[0], xa, xb, src);
+    if constexpr (BTR)
+      kstep_t<0>(acc, P, Q[1], Q[0], xa, xb, src);
+    else
+      kstep<0>(acc, P, Q[1], Q[0], xa, xb, src);
 
     if (++e_kt < e_kn) continue;
     // ---- tile epilogue: this wave's 64 x 128 block
@@ -937,7 +964,7 @@ __device__ __forceinline__ void store_grad(const WgradArgs& a, int g, int m, int
 // column 4 q): two such reads give a lane 8 consecutive k of one output row.
 // The 32-byte windows of a k row are XOR-swizzled by wsw(row) so that the 16
 // rows x 32 bytes a read instruction touches fall on distinct banks.
-__device__ __forceinline__ int wsw(int r) { return (r & 3) | (((r >> 3) & 1) << 2); }
+using core::wsw;
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ bf16x8 tr_frag(uint32_t addr) {
@@ -1354,16 +1381,16 @@ extern "C" int fmoe_down_fwd(const void* h, const int32_t* offsets, int n_expert
 
 extern "C" int fmoe_down_bwd_dx(const void* d_out_routed, const void* d_out_shared,
                                 const int32_t* offsets, int n_experts, int64_t rows_routed,
-                                int64_t rows_shared, int64_t dim, int64_t inter, const void* w2t,
+                                int64_t rows_shared, int64_t dim, int64_t inter, const void* const* w2,
                                 const void* ab, void* d_ab, void* workspace, size_t workspace_bytes,
                                 void* stream) {
   int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
   if (st) return st;
   if (rows_routed + rows_shared == 0) return FMOE_OK;
-  if (!offsets || !w2t || !ab || !d_ab || (rows_routed && !d_out_routed) ||
+  if (!offsets || !w2 || !ab || !d_ab || (rows_routed && !d_out_routed) ||
       (rows_shared && !d_out_shared))
     return FMOE_ERR_INVALID_ARG;
-  if (!aligned16(w2t) || !aligned16(ab) || !aligned16(d_ab)) return FMOE_ERR_ALIGN;
+  if (!aligned16(ab) || !aligned16(d_ab)) return FMOE_ERR_ALIGN;
   GemmArgs a = {};
   a.a_routed = static_cast<const uint16_t*>(d_out_routed);
   a.a_shared = static_cast<const uint16_t*>(d_out_shared);
@@ -1372,26 +1399,30 @@ extern "C" int fmoe_down_bwd_dx(const void* d_out_routed, const void* d_out_shar
   a.K = static_cast<int>(dim);
   a.N = static_cast<int>(inter);
   a.inter = static_cast<int>(inter);
-  a.ldb = dim;  // w2t[g] is [inter, dim]: row n = inter index, K = dim contiguous
+  a.ldb = inter;  // w2[g] is [dim, inter] as nn.Linear keeps it: k row = dim index, inter contiguous
   a.c0 = static_cast<uint16_t*>(d_ab);
   a.ldc0 = 2 * inter;
   a.aux = static_cast<const uint16_t*>(ab);
   a.ldaux = 2 * inter;
   a.split_ws = (workspace && workspace_bytes >= fmoe_split_workspace_bytes()) ? static_cast<float*>(workspace) : nullptr;
   const int G = n_experts + (rows_shared > 0 ? 1 : 0);
-  for (int g = 0; g < G; ++g) a.b0[g] = static_cast<const uint16_t*>(w2t) + static_cast<int64_t>(g) * inter * dim;
+  for (int g = 0; g < G; ++g) {
+    if (!w2[g]) return FMOE_ERR_INVALID_ARG;
+    if (!aligned16(w2[g])) return FMOE_ERR_ALIGN;
+    a.b0[g] = static_cast<const uint16_t*>(w2[g]);
+  }
   return launch_rows<DOWN_BWD>(a, rows_routed, rows_shared, n_experts, stream);
 }
 
 extern "C" int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int n_experts,
                                   int64_t rows_routed, int64_t rows_shared, int64_t dim,
-                                  int64_t inter, const void* w13t, void* dx_rows, void* workspace,
-                                  size_t workspace_bytes, void* stream) {
+                                  int64_t inter, const void* const* w1, const void* const* w3, void* dx_rows,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
   int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
   if (st) return st;
   if (rows_routed + rows_shared == 0) return FMOE_OK;
-  if (!d_ab || !offsets || !w13t || !dx_rows) return FMOE_ERR_INVALID_ARG;
-  if (!aligned16(d_ab) || !aligned16(w13t) || !aligned16(dx_rows)) return FMOE_ERR_ALIGN;
+  if (!d_ab || !offsets || !w1 || !w3 || !dx_rows) return FMOE_ERR_INVALID_ARG;
+  if (!aligned16(d_ab) || !aligned16(dx_rows)) return FMOE_ERR_ALIGN;
   GemmArgs a = {};
   a.a_routed = static_cast<const uint16_t*>(d_ab);
   a.a_shared = nullptr;
@@ -1400,13 +1431,17 @@ extern "C" int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int 
   a.K = static_cast<int>(2 * inter);
   a.N = static_cast<int>(dim);
   a.inter = static_cast<int>(inter);
-  a.ldb = 2 * inter;  // w13t[g] is [dim, 2*inter]: row n = dim index, K = 2*inter contiguous
+  a.ldb = dim;  // w1[g], w3[g] are [inter, dim]: k rows 0..inter-1 from w1, inter.. from w3
   a.c0 = static_cast<uint16_t*>(dx_rows);
   a.ldc0 = dim;
   a.split_ws = (workspace && workspace_bytes >= fmoe_split_workspace_bytes()) ? static_cast<float*>(workspace) : nullptr;
   const int G = n_experts + (rows_shared > 0 ? 1 : 0);
-  for (int g = 0; g < G; ++g)
-    a.b0[g] = static_cast<const uint16_t*>(w13t) + static_cast<int64_t>(g) * dim * 2 * inter;
+  for (int g = 0; g < G; ++g) {
+    if (!w1[g] || !w3[g]) return FMOE_ERR_INVALID_ARG;
+    if (!aligned16(w1[g]) || !aligned16(w3[g])) return FMOE_ERR_ALIGN;
+    a.b0[g] = static_cast<const uint16_t*>(w1[g]);
+    a.b1[g] = static_cast<const uint16_t*>(w3[g]);
+  }
   return launch_rows<GATEUP_BWD>(a, rows_routed, rows_shared, n_experts, stream);
 }
 

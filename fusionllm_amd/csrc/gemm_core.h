@@ -151,5 +151,79 @@ __device__ __forceinline__ void kstep(f32x4 (&acc)[FM][FN], bf16x8 (&P)[FN], bf1
             frag_addr<7, KX>(xb, srcb));
 }
 
+// ---- weights read as they lie ([K, N] row-major, N contiguous): the backward
+// dX products (dh = d_out * w2, dx = [da | db] * [w1; w3]) take their B
+// operand from the nn.Linear weights without a transposed copy.
+// B stage: 64 k rows of 512 bytes (256 n values), copied as they lie; the
+// 32-byte windows of a k row are XOR-swizzled by wsw(k row), and fragments
+// are read with ds_read_b64_tr_b16, which returns to lane (h = l / 16,
+// i = l % 16) column i of the 4 x 4 block of 16-bit values that the
+// group's source lanes 4 j + q address (row j, 4 values at column 4 q); two
+// such reads, 4 k rows apart, give a lane 8 consecutive k of one n.  A
+// 64-bit read cannot name half of an inline-assembly operand, so in this
+// variant all LDS reads are compiler loads (the compiler places the waits
+// for them) and only the MFMA groups are inline assembly.
+__device__ __forceinline__ int wsw(int r) { return (r & 3) | (((r >> 3) & 1) << 2); }
+
+// Lane's address of B fragment 0 (K half 0) within a stage, relative to the
+// stage base: k row 8 h + jq (+4 for the second read), window (8 wn + fr) for
+// the wave's 128 columns, fr = wsw(8 h + jq).  Fragment f: ^ (f << 5); the
+// second 32-deep half of the stage: + 32 rows.
+__device__ __forceinline__ uint32_t trb_base(int wn, int lane) {
+  const int h = lane >> 4, jq = (lane >> 2) & 3, q = lane & 3;
+  const int fr = jq | ((h & 1) << 2);
+  return static_cast<uint32_t>(A_BYTES + (8 * h + jq) * 512 + ((8 * wn + fr) << 5) + 8 * q);
+}
+constexpr uint32_t TRB_KHALF = 32 * 512;
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+// One B fragment: 8 consecutive k of the lane's n (two transposing reads).
+__device__ __forceinline__ bf16x8 trb_frag(uint32_t addr) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)addr);
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)(addr + 2048u));
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+#define FMOE_MFA(c, a, b) "v_mfma_f32_16x16x32_bf16 " c ", " a ", " b ", " c "\n"
+// Four MFMAs of one B fragment: acc[0..3][j] += P[j] (x) Q[0..3].  The LDS
+// reads of this variant are compiler loads, so the compiler places exact
+// waits for them before the statement that consumes them.
+__device__ __forceinline__ void block4m(f32x4& c0, f32x4& c1, f32x4& c2, f32x4& c3, const bf16x8& p,
+                                        const bf16x8& q0, const bf16x8& q1, const bf16x8& q2, const bf16x8& q3) {
+  asm volatile(FMOE_MFA("%[c0]", "%[p]", "%[q0]") FMOE_MFA("%[c1]", "%[p]", "%[q1]")
+               FMOE_MFA("%[c2]", "%[p]", "%[q2]") FMOE_MFA("%[c3]", "%[p]", "%[q3]")
+               : [c0] "+v"(c0), [c1] "+v"(c1), [c2] "+v"(c2), [c3] "+v"(c3)
+               : [p] "v"(p), [q0] "v"(q0), [q1] "v"(q1), [q2] "v"(q2), [q3] "v"(q3)
+               : "memory");
+}
+#undef FMOE_MFA
+
+// kstep with B read as it lies.  Block x: MFMAs with P[2x], then the next
+// step's Q'[x] (A side, double buffered) and P[2x] (in place), MFMAs with
+// P[2x+1], then P[2x+1].  KH: the next fragments come from the second (1) or
+// first (0) 32-deep half of the stage at src.  (Measured against the
+// transposed-copy path on MI355X, outputs bit-identical: the two dX products
+// 1 % slower at C2 and 2 % at C5, less than the transposed copies cost.)
+template <int KH>
+__device__ __forceinline__ void kstep_t(f32x4 (&acc)[FM][FN], bf16x8 (&P)[FN], bf16x8 (&Qc)[4], bf16x8 (&Qn)[4],
+                                        uint32_t xa, uint32_t xbt, uint32_t src) {
+  constexpr int KX = KH ? 64 : 0;
+  const uint32_t bb = src + (KH ? TRB_KHALF : 0u);
+  typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
+#define FMOE_BLK(X)                                                                                              \
+  block4m(acc[0][2 * X], acc[1][2 * X], acc[2][2 * X], acc[3][2 * X], P[2 * X], Qc[0], Qc[1], Qc[2], Qc[3]);        \
+  Qn[X] = *(const lds_bf16x8*)(uintptr_t)frag_addr<X, KX>(xa, src);                                                \
+  P[2 * X] = trb_frag(bb + (xbt ^ ((2u * X) << 5)));                                                              \
+  block4m(acc[0][2 * X + 1], acc[1][2 * X + 1], acc[2][2 * X + 1], acc[3][2 * X + 1], P[2 * X + 1], Qc[0], Qc[1],  \
+          Qc[2], Qc[3]);                                                                                          \
+  P[2 * X + 1] = trb_frag(bb + (xbt ^ ((2u * X + 1) << 5)));
+  FMOE_BLK(0)
+  FMOE_BLK(1)
+  FMOE_BLK(2)
+  FMOE_BLK(3)
+#undef FMOE_BLK
+}
+
 }  // namespace core
 }  // namespace fmoe

@@ -120,13 +120,12 @@ def _dense_backward(dy, xb, ab, h, w1b, w3b, w2b, off, dtypes, need_dx):
     T, d = xb.shape
     inter = w1b.shape[0]
     dyb = _as_bf16(dy).contiguous()
-    w13t, w2t = K.transpose_weights([w1b], [w3b], [w2b])
-    d_ab = K.down_bwd_dx(dyb, None, off, 1, w2t, ab, inter)
+    d_ab = K.down_bwd_dx(dyb, None, off, 1, [w2b], ab, inter)
     dw2 = torch.empty(d, inter, dtype=w2_dtype, device=xb.device)
     K.weight_grad(dyb, None, h, None, off, 1, T, 0, d, [dw2], None, w2_dtype, tag="w2")
     dx = None
     if need_dx:
-        dx = K.gateup_bwd_dx(d_ab, off, 1, T, 0, w13t, d)
+        dx = K.gateup_bwd_dx(d_ab, off, 1, T, 0, [w1b], [w3b], d)
         if dx.dtype != x_dtype:
             dx = dx.to(x_dtype)
     dw1 = torch.empty(inter, d, dtype=w1_dtype, device=xb.device)
@@ -314,15 +313,14 @@ def _backward_pass(ctx, saved, dy):
     d_o, d_w = K.combine_bwd(dy, o, w, perm, k)
     dy_sh = _as_bf16(dy).contiguous() if has_shared else None
 
-    # Transposed weight copies for the dX products (one launch for all groups).
-    w13t, w2t = K.transpose_weights(w1s, w3s, w2s)
-    # Down projection: dX with the SwiGLU backward fused, then dW2.
-    d_ab = K.down_bwd_dx(d_o, dy_sh, offsets, E, w2t, ab, inter)
+    # Down projection: dX with the SwiGLU backward fused (reading w2 as it
+    # lies), then dW2.
+    d_ab = K.down_bwd_dx(d_o, dy_sh, offsets, E, w2s, ab, inter)
     dw2 = [torch.empty(d, inter, dtype=w_dtypes[3 * g + 2], device=xb.device) for g in range(G)]
     K.weight_grad(d_o, dy_sh, h, None, offsets, E, rows_r, rows_s, d, dw2, None,
                   w_dtypes[2], tag="w2")
     # Gate/up projections: dX (one product over [w1; w3]) then dW1, dW3.
-    dx_rows = K.gateup_bwd_dx(d_ab, offsets, E, rows_r, rows_s, w13t, d)
+    dx_rows = K.gateup_bwd_dx(d_ab, offsets, E, rows_r, rows_s, w1s, w3s, d)
     dw1 = [torch.empty(inter, d, dtype=w_dtypes[3 * g], device=xb.device) for g in range(G)]
     dw3 = [torch.empty(inter, d, dtype=w_dtypes[3 * g + 1], device=xb.device) for g in range(G)]
     K.weight_grad(d_ab, None, x_perm, xb if has_shared else None, offsets, E, rows_r, rows_s,

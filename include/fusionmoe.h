@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define FMOE_ABI_VERSION 11
+#define FMOE_ABI_VERSION 12
 #define FMOE_MAX_EXPERTS 64
 #define FMOE_MAX_TOPK 8
 #define FMOE_MAX_CAST 64
@@ -222,34 +222,34 @@ int fmoe_combine_bwd(const void* dy, int dy_dtype, const void* expert_out,
 
 /* ---------------------------------------------------------------------------
  * Backward of SwiGLUExpert (autograd of models/moe.py:21), grouped like the
- * forward.  The dX products multiply by the weights along their output
- * dimension, so they read transposed copies made once per backward pass:
- *   w2t  [G, inter, dim]       w2t[g]  = w2[g]^T
- *   w13t [G, dim, 2*inter]     w13t[g] = [w1[g]; w3[g]]^T
- * (G = routed experts + shared expert; caller-allocated, contiguous).
+ * forward.  The dX products read the nn.Linear weights as they lie
+ * (models/moe.py:16-18: w1, w3 [inter, dim], w2 [dim, inter]), one pointer
+ * per group (G = routed experts + shared expert), 16-byte aligned.
  * ------------------------------------------------------------------------- */
-int fmoe_transpose_weights(const void* const* w1, const void* const* w3,
-                           const void* const* w2, int n_groups, int64_t dim,
-                           int64_t inter, void* w13t, void* w2t, void* stream);
 
 /* dh = d_out w2 (bf16-rounded), then the SwiGLU backward in the epilogue:
  *   da = bf16(bf16(dh*b) * silu'(a)),  db = bf16(dh * bf16(silu(a))).
  * d_out_routed: [rows_routed, dim]; d_out_shared: [rows_shared, dim];
- * ab from fmoe_gateup_fwd; d_ab: [rows, 2*inter];
- * workspace: see fmoe_split_workspace_bytes. */
+ * w2[g]: [dim, inter]; ab from fmoe_gateup_fwd; d_ab: [rows, 2*inter];
+ * workspace: see fmoe_split_workspace_bytes.
+ * Replaces the autograd of self.w2(...) in SwiGLUExpert.forward (models/moe.py:21). */
 int fmoe_down_bwd_dx(const void* d_out_routed, const void* d_out_shared,
                      const int32_t* offsets, int n_experts,
                      int64_t rows_routed, int64_t rows_shared,
-                     int64_t dim, int64_t inter, const void* w2t,
+                     int64_t dim, int64_t inter, const void* const* w2,
                      const void* ab, void* d_ab, void* workspace, size_t workspace_bytes,
                      void* stream);
 
 /* dx_rows = da w1 + db w3 for every row (one product over K = 2*inter);
- * dx_rows: [rows, dim] bf16; workspace: see fmoe_split_workspace_bytes. */
+ * w1[g], w3[g]: [inter, dim]; dx_rows: [rows, dim] bf16;
+ * workspace: see fmoe_split_workspace_bytes.
+ * Replaces the input-gradient half of the autograd of self.w1(x), self.w3(x)
+ * (models/moe.py:21). */
 int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int n_experts,
                        int64_t rows_routed, int64_t rows_shared,
-                       int64_t dim, int64_t inter, const void* w13t,
-                       void* dx_rows, void* workspace, size_t workspace_bytes, void* stream);
+                       int64_t dim, int64_t inter, const void* const* w1,
+                       const void* const* w3, void* dx_rows, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 /* Grouped weight gradient, the dW half of nn.Linear backward for every expert:
  *   G_e = A_e^T B_e,  A_e = rows of expert e of A ([*, m_out]),

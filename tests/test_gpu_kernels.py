@@ -359,8 +359,13 @@ def test_gateup_and_down_fwd(gpu_device, counts, shared, d, I):
         close(o[r0:r1], o_ref, rtol=8e-3, atol=1e-3)
 
 
-@pytest.mark.parametrize("counts,shared,d,I", [([0, 300, 517], 400, 192, 320), ([100, 1, 2000], 700, 768, 2048)])
+@pytest.mark.parametrize("counts,shared,d,I", [([0, 300, 517], 400, 192, 320), ([100, 1, 2000], 700, 768, 2048),
+                                               ([40, 300, 700], 200, 320, 1408)])
 def test_backward_products(gpu_device, counts, shared, d, I):
+    # The dX products read the nn.Linear weights as they lie (w2 [d, I],
+    # w1 / w3 [I, d]) through transposing LDS reads; partial n tiles
+    # (I = 320, 1408; d = 192, 320) and a single 64-deep K stage per tile are
+    # covered.
     g = torch.Generator().manual_seed(2)
     E = len(counts)
     offsets, rows_r = _groups(counts, gpu_device)
@@ -377,9 +382,8 @@ def test_backward_products(gpu_device, counts, shared, d, I):
     w2 = [_bf(d, I, scale=0.05, g=g) for _ in range(G)]
     D = gpu_device
     dv = lambda ts: [t.to(D) for t in ts]
-    w13t, w2t = K.transpose_weights(dv(w1), dv(w3), dv(w2))
-    d_ab = K.down_bwd_dx(do_r.to(D), do_s.to(D) if shared else None, offsets, E, w2t, ab.to(D), I)
-    dx_rows = K.gateup_bwd_dx(d_ab, offsets, E, rows_r, shared, w13t, d)
+    d_ab = K.down_bwd_dx(do_r.to(D), do_s.to(D) if shared else None, offsets, E, dv(w2), ab.to(D), I)
+    dx_rows = K.gateup_bwd_dx(d_ab, offsets, E, rows_r, shared, dv(w1), dv(w3), d)
     dw2 = [torch.empty(d, I, dtype=torch.bfloat16, device=D) for _ in range(G)]
     K.weight_grad(do_r.to(D), do_s.to(D) if shared else None, h.to(D), None, offsets, E, rows_r, shared,
                   d, dw2, None, torch.bfloat16)
@@ -417,7 +421,7 @@ def test_backward_products(gpu_device, counts, shared, d, I):
         assert rel_l2(dw3[grp].cpu(), dw3_ref) < 1e-5
 
 
-def _row_products(D, x_r, x_s, do_r, do_s, offsets, E, w1, w3, w2, w13t, w2t, ab_in, h_in, dab_in, split,
+def _row_products(D, x_r, x_s, do_r, do_s, offsets, E, w1, w3, w2, ab_in, h_in, dab_in, split,
                   short_ws=False):
     """The four row products through the C ABI, with the split workspace or
     without it (short_ws: a workspace one byte smaller than the query asks
@@ -446,11 +450,11 @@ def _row_products(D, x_r, x_s, do_r, do_s, offsets, E, w1, w3, w2, w13t, w2t, ab
                                  o.data_ptr(), wsp, ws_bytes, st), "down_fwd")
     d_ab = torch.empty(rows, 2 * I, dtype=torch.bfloat16, device=D)
     _lib.check(lib.fmoe_down_bwd_dx(do_r.data_ptr(), do_s.data_ptr(), offsets.data_ptr(), E, rows_r, rows_s, d, I,
-                                    w2t.data_ptr(), ab_in.data_ptr(), d_ab.data_ptr(), wsp, ws_bytes, st),
+                                    pa(w2), ab_in.data_ptr(), d_ab.data_ptr(), wsp, ws_bytes, st),
                "down_bwd_dx")
     dx = torch.empty(rows, d, dtype=torch.bfloat16, device=D)
     _lib.check(lib.fmoe_gateup_bwd_dx(dab_in.data_ptr(), offsets.data_ptr(), E, rows_r, rows_s, d, I,
-                                      w13t.data_ptr(), dx.data_ptr(), wsp, ws_bytes, st), "gateup_bwd_dx")
+                                      pa(w1), pa(w3), dx.data_ptr(), wsp, ws_bytes, st), "gateup_bwd_dx")
     return [t.cpu() for t in (ab, h, o, d_ab, dx)]
 
 
@@ -478,8 +482,7 @@ def test_split_tail_matches_whole_tiles(gpu_device):
     w1 = [_bf(I, d, scale=0.05, g=g).to(D) for _ in range(G)]
     w3 = [_bf(I, d, scale=0.05, g=g).to(D) for _ in range(G)]
     w2 = [_bf(d, I, scale=0.05, g=g).to(D) for _ in range(G)]
-    w13t, w2t = K.transpose_weights(w1, w3, w2)
-    args = (D, x_r, x_s, do_r, do_s, offsets, E, w1, w3, w2, w13t, w2t, ab_in, h_in, dab_in)
+    args = (D, x_r, x_s, do_r, do_s, offsets, E, w1, w3, w2, ab_in, h_in, dab_in)
     split = _row_products(*args, split=True)
     whole = _row_products(*args, split=False)
     # a workspace smaller than the query runs every tile whole
@@ -501,20 +504,6 @@ def test_split_tail_matches_whole_tiles(gpu_device):
     dag, dbg = dab_in[rows_r:, :I].cpu().float(), dab_in[rows_r:, I:].cpu().float()
     dx_ref = dag @ w1[E].cpu().float() + dbg @ w3[E].cpu().float()
     close(split[4][rows_r:], dx_ref, rtol=1e-2, atol=2e-3)
-
-
-@pytest.mark.parametrize("G,d,I", [(9, 768, 2048), (2, 64, 192), (3, 192, 64)])
-def test_transpose_weights_bit_exact(gpu_device, G, d, I):
-    g = torch.Generator().manual_seed(G)
-    w1 = [_bf(I, d, g=g) for _ in range(G)]
-    w3 = [_bf(I, d, g=g) for _ in range(G)]
-    w2 = [_bf(d, I, g=g) for _ in range(G)]
-    dv = lambda ts: [t.to(gpu_device) for t in ts]
-    w13t, w2t = K.transpose_weights(dv(w1), dv(w3), dv(w2))
-    want13 = torch.stack([torch.cat([a, b]).T for a, b in zip(w1, w3)])
-    want2 = torch.stack([w.T for w in w2])
-    assert torch.equal(w13t.cpu().view(torch.int16), want13.contiguous().view(torch.int16))
-    assert torch.equal(w2t.cpu().view(torch.int16), want2.contiguous().view(torch.int16))
 
 
 def test_cast_bf16_bit_exact(gpu_device):
