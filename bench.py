@@ -89,8 +89,11 @@ def kernel_model(cfg, T, active_groups=None):
     forward products by HBM bytes: the weights of the active_groups groups
     that received rows (shared expert included), read once, plus the
     activation rows in and out."""
+    from fusionllm_amd.moe import gathers_rows
     d, I, E, k = cfg.dim, cfg.inter, cfg.n_experts, cfg.topk
     rows = T * k + (T if cfg.n_shared else 0)
+    # the k gathered rows per token (x_perm), unless the block reads token rows through perm
+    xp = 0 if gathers_rows(T, k, cfg.n_shared > 0) else k * 2 * d
     if T <= 128 and active_groups is not None:
         return {
             "gateup_fwd": ("hbm", active_groups * 2 * I * d * 2 + rows * (d + 3 * I) * 2),
@@ -111,13 +114,14 @@ def kernel_model(cfg, T, active_groups=None):
         "weight_grad:w13": ("mfma", 2.0 * rows * 2 * I * d),
         # HBM-bound (algorithmic bytes: bf16 activations, int32/fp32 metadata)
         "router_fwd": ("hbm", T * (2 * d + 4 * k + 8 * k + 4 * k + 4 * k)),
-        "dispatch": ("hbm", T * (4 * k + 2 * d + k * 2 * d + 8 * k + 4 * k)),
+        "dispatch": ("hbm", T * (4 * k + (2 * d + xp if xp else 0) + 8 * k + 4 * k)),
         "combine_fwd": ("hbm", T * (k * 2 * d + 2 * d + 8 * k + 4 * k + 2 * d)),
         "combine_bwd": ("hbm", T * k * (2 * d + 2 * d + 2 * d + 4 + 4 + 4)),
         "router_bwd": ("hbm", T * k * (2 * d + 4 * 4)),
         # routing + dispatch in one entry point: x read once; idx, idx64, weights, scores,
-        # perm, pos and the k rows of x_perm written
-        "route_and_dispatch": ("hbm", T * (2 * d + 4 * k + 8 * k + 4 * k + 4 * k + 4 * k + 4 * k + k * 2 * d)),
+        # perm and pos written (and the k rows of x_perm when the block keeps the gathered copy)
+        "route_and_dispatch": ("hbm", T * (2 * d + 4 * k + 8 * k + 4 * k + 4 * k + 4 * k + 4 * k
+                                           + xp)),
         "dx_reduce": ("hbm", T * (k * 2 * d + 2 * d + 2 * d + 12 * k)),
         # C4 (RMSNorm + MoE + residual): x in, xn and rstd out; the backward
         # reads the k routed + shared rows, x and d_out and writes dx
@@ -152,8 +156,9 @@ def graph_entry_times(m, x, reps=20, replays=20):
         calls = {"router_fwd": lambda: K.router_fwd(xb, gwb, gbb, k, float(m.route_scale)),
                  "dispatch": lambda: K.dispatch(idx, xb, E)}
     calls.update({
-        "gateup_fwd": lambda: K.gateup_fwd(x_perm, xb if has_shared else None, offsets, E, w1s, w3s,
-                                           m.moe_inter_dim),
+        "gateup_fwd": lambda: K.gateup_fwd(xb if x_perm is None else x_perm, xb if has_shared else None, offsets,
+                                           E, w1s, w3s, m.moe_inter_dim, gather=perm if x_perm is None else None,
+                                           k=k),
         "down_fwd": lambda: K.down_fwd(h, offsets, E, rows_r, rows_s, w2s, d),
         "combine_fwd": lambda: K.combine_fwd(o, idx, w, pos, rows_r, has_shared, x.dtype, None),
     })
@@ -208,15 +213,15 @@ def graph_hbm_times(m, x, dy):
         gbb = m.gate.bias.to(torch.bfloat16).contiguous()
         dyb = dy.to(torch.bfloat16).contiguous()
         d_o, d_w = K.combine_bwd(dyb, o, w, perm, k)
-        d_logits, _, _ = K.router_bwd(d_w, v, perm, offsets, x_perm, E, rs, m.gate.weight.dtype)
+        d_logits, _, _ = K.router_bwd(d_w, v, perm, offsets, xb, E, rs, m.gate.weight.dtype)
         dx_rows = torch.empty(o.shape, dtype=torch.bfloat16, device=o.device).normal_()
         calls = {
             "router_fwd": lambda: K.router_fwd(xb, gwb, gbb, k, rs),
-            "dispatch": lambda: K.dispatch(idx, xb, E),
+            "dispatch": lambda: K.dispatch(idx, xb, E, gather=x_perm is not None),
             "combine_fwd": lambda: K.combine_fwd(o, idx, w, pos, T * k, has_shared, x.dtype, None),
             "combine_bwd": lambda: K.combine_bwd(dyb, o, w, perm, k),
-            "router_bwd": lambda: K.router_bwd(d_w, v, perm, offsets, x_perm, E, rs, m.gate.weight.dtype),
-            "route_and_dispatch": lambda: K.route_and_dispatch(xb, gwb, gbb, k, rs),
+            "router_bwd": lambda: K.router_bwd(d_w, v, perm, offsets, xb, E, rs, m.gate.weight.dtype),
+            "route_and_dispatch": lambda: K.route_and_dispatch(xb, gwb, gbb, k, rs, gather=x_perm is not None),
             "dx_reduce": lambda: K.dx_reduce(dx_rows, pos, idx, d_logits, gwb, T * k, has_shared, x.dtype),
         }
         return {name: graph_time(fn) for name, fn in calls.items()}
@@ -657,7 +662,8 @@ def main():
                    "pass": "forward" if args.fwd_only else "forward+backward",
                    "launch": "hip-graph replay" if args.graph else "eager",
                    "params": "fp32 under bf16 autocast" if args.autocast else "bf16"},
-        "grouped_gemm_mfma_frac": round(gemm_flops / gemm_s / PEAK_BF16_FLOPS, 4),
+        # (null when the step runs no separate GEMM entry point: the fused decode forward)
+        "grouped_gemm_mfma_frac": round(gemm_flops / gemm_s / PEAK_BF16_FLOPS, 4) if gemm_s > 0 else None,
         "step_mfma_frac": round(gemm_flops / (elapsed / args.steps) / PEAK_BF16_FLOPS, 4),
         "roofline": roofline,
         "kernels": kernels,

@@ -204,16 +204,22 @@ def dispatch(idx, x, n_experts: int, gather: bool = True, noalloc: bool = False)
 
 
 @_timed
-def gateup_fwd(x_perm, x_shared, offsets, n_experts: int, w1s, w3s, inter: int):
+def gateup_fwd(x_rows, x_shared, offsets, n_experts: int, w1s, w3s, inter: int, gather=None, k: int = 1):
+    """a|b and h of every routed and shared row.  x_rows: the routed rows [T*k, dim] (x_perm), or,
+    with gather (the dispatch's perm, row -> slot t*k + j), the token rows x [T, dim], routed row r
+    reading x row gather[r] // k (launches of more than SMALL_LAUNCH_ROWS rows)."""
     lib = _lib.load()
-    rows_r, d = x_perm.shape
+    d = x_rows.shape[1]
+    rows_r = gather.numel() if gather is not None else x_rows.shape[0]
     rows_s = x_shared.shape[0] if x_shared is not None else 0
-    dev = x_perm.device
+    dev = x_rows.device
     rows = rows_r + rows_s
     ab = torch.empty(rows, 2 * inter, dtype=torch.bfloat16, device=dev)
     h = torch.empty(rows, inter, dtype=torch.bfloat16, device=dev)
     ws, ws_bytes = _split_workspace(dev, rows_r, rows_s, -(-inter // 128), small=True)
-    check(lib.fmoe_gateup_fwd(_req(x_perm, "x_perm", torch.bfloat16),
+    check(lib.fmoe_gateup_fwd(_req(x_rows, "x_rows", torch.bfloat16),
+                              _req(gather, "gather", torch.int32) if gather is not None else None, int(k),
+                              x_rows.shape[0],
                               _req(x_shared, "x", torch.bfloat16) if x_shared is not None else None,
                               _req(offsets, "offsets", torch.int32), n_experts, rows_r, rows_s, d, inter,
                               ptr_array([w.data_ptr() for w in w1s]), ptr_array([w.data_ptr() for w in w3s]),
@@ -345,8 +351,11 @@ def gateup_bwd_dx(d_ab, offsets, n_experts: int, rows_routed: int, rows_shared: 
 
 @_timed
 def weight_grad(a_routed, a_shared, b_routed, b_shared, offsets, n_experts: int, rows_routed: int,
-                rows_shared: int, m_split: int, outs_lo, outs_hi, out_dtype: torch.dtype):
-    """G_e = A_e^T B_e for every group, written into outs_lo[e] / outs_hi[e]."""
+                rows_shared: int, m_split: int, outs_lo, outs_hi, out_dtype: torch.dtype, b_gather=None,
+                k: int = 1):
+    """G_e = A_e^T B_e for every group, written into outs_lo[e] / outs_hi[e].  With b_gather (the
+    dispatch's perm), b_routed is the token rows x [T, n_out] and routed row r of B is x row
+    b_gather[r] // k."""
     lib = _lib.load()
     m_out = a_routed.shape[1]
     n_out = b_routed.shape[1]
@@ -360,6 +369,8 @@ def weight_grad(a_routed, a_shared, b_routed, b_shared, offsets, n_experts: int,
                                _req(b_routed, "B", torch.bfloat16),
                                _req(b_shared, "B_shared", torch.bfloat16) if b_shared is not None else None,
                                b_routed.stride(0),
+                               _req(b_gather, "b_gather", torch.int32) if b_gather is not None else None, int(k),
+                               b_routed.shape[0],
                                _req(offsets, "offsets", torch.int32), n_experts, rows_routed, rows_shared,
                                m_out, n_out, m_split, lo, hi, _dtype_code(out_dtype),
                                ws.data_ptr(), ws_bytes, _stream()),
@@ -367,10 +378,11 @@ def weight_grad(a_routed, a_shared, b_routed, b_shared, offsets, n_experts: int,
 
 
 @_timed
-def router_bwd(d_w, topv, perm, offsets, x_perm, n_experts: int, route_scale: float, grad_dtype: torch.dtype):
+def router_bwd(d_w, topv, perm, offsets, x, n_experts: int, route_scale: float, grad_dtype: torch.dtype):
+    """Logit gradients and the gate's weight / bias gradients; x: [T, dim] bf16 token rows (read through perm)."""
     lib = _lib.load()
     T, k = d_w.shape
-    d = x_perm.shape[1]
+    d = x.shape[1]
     dev = d_w.device
     d_logits = torch.empty(T, k, dtype=torch.float32, device=dev)
     dgw = torch.empty(n_experts, d, dtype=grad_dtype, device=dev)
@@ -379,7 +391,7 @@ def router_bwd(d_w, topv, perm, offsets, x_perm, n_experts: int, route_scale: fl
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
     check(lib.fmoe_router_bwd(_req(d_w, "d_weights", torch.float32), _req(topv, "topv", torch.float32),
                               _req(perm, "perm", torch.int32), _req(offsets, "offsets", torch.int32),
-                              _req(x_perm, "x_perm", torch.bfloat16), T, d, n_experts, k, float(route_scale),
+                              _req(x, "x", torch.bfloat16), T, d, n_experts, k, float(route_scale),
                               d_logits.data_ptr(), dgw.data_ptr(), dgb.data_ptr(), _dtype_code(grad_dtype),
                               ws.data_ptr(), ws_bytes, _stream()),
           "fmoe_router_bwd")

@@ -13,7 +13,7 @@ from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int64, c_size_
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libfusionmoe.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 MAX_EXPERTS = 64
 MAX_TOPK = 8
 
@@ -37,7 +37,7 @@ SIGNATURES = {
     "fmoe_route_and_dispatch_workspace_bytes": (c_size_t, [c_int64, c_int, c_int]),
     "fmoe_route_and_dispatch": (c_int, [_P, _P, _P, c_int64, c_int64, c_int, c_int, c_float,
                                         _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_size_t, _P]),
-    "fmoe_gateup_fwd": (c_int, [_P, _P, _P, c_int, c_int64, c_int64, c_int64, c_int64,
+    "fmoe_gateup_fwd": (c_int, [_P, _P, c_int, c_int64, _P, _P, c_int, c_int64, c_int64, c_int64, c_int64,
                                 _PP, _PP, _P, _P, _P, c_size_t, _P]),
     "fmoe_split_workspace_bytes": (c_size_t, []),
     "fmoe_down_fwd": (c_int, [_P, _P, c_int, c_int64, c_int64, c_int64, c_int64,
@@ -51,7 +51,7 @@ SIGNATURES = {
     "fmoe_gateup_bwd_dx": (c_int, [_P, _P, c_int, c_int64, c_int64, c_int64, c_int64,
                                    _PP, _PP, _P, _P, c_size_t, _P]),
     "fmoe_weight_grad_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int, c_int64, c_int64]),
-    "fmoe_weight_grad": (c_int, [_P, _P, c_int64, _P, _P, c_int64, _P, c_int,
+    "fmoe_weight_grad": (c_int, [_P, _P, c_int64, _P, _P, c_int64, _P, c_int, c_int64, _P, c_int,
                                  c_int64, c_int64, c_int64, c_int64, c_int64,
                                  _PP, _PP, c_int, _P, c_size_t, _P]),
     "fmoe_router_bwd_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int, c_int]),

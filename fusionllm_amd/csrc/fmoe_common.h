@@ -104,6 +104,17 @@ __device__ __forceinline__ bool score_beats(float a, float b) {
   return a > b;
 }
 
+// Token of a routed slot, floor(n / k) for 0 <= n < 2^29 and 1 <= k <= 8,
+// without a division: the high half of n * m with m = ceil(2^32 / k).  With
+// m k = 2^32 + e, 0 <= e < k, n m / 2^32 = n / k + n e / (k 2^32); the
+// excess stays below 1 / k (n e < 2^32), and the fraction of n / k is at most
+// (k - 1) / k, so the floor is exact.  m = 2^32 (k = 1) does not fit 32 bits:
+// magic holds m mod 2^32 and the product adds n * (m >> 32), with no branch.
+inline uint64_t slot_div_magic(int k) { return ((uint64_t(1) << 32) + k - 1) / k; }
+__device__ __forceinline__ uint32_t slot_token(uint32_t n, uint64_t magic) {
+  return __umulhi(n, static_cast<uint32_t>(magic)) + n * static_cast<uint32_t>(magic >> 32);
+}
+
 // ---- status helpers (host) --------------------------------------------------
 inline int launch_status() {
   hipError_t e = hipGetLastError();

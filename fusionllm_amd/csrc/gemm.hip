@@ -45,7 +45,11 @@ namespace fmoe {
 enum GemmMode { GATEUP_FWD = 0, DOWN_FWD = 1, DOWN_BWD = 2, GATEUP_BWD = 3 };
 
 struct GemmArgs {
-  const uint16_t* a_routed;  // [rows_routed, K]
+  const uint16_t* a_routed;  // [rows_routed, K], or with gather: x [T, K]
+  const int32_t* gather;     // GATEUP_FWD tiled kernel: routed row r reads a_routed row gather[r] / gather_k
+                             // (nullptr: row r; launches of more than kSmallLaunchRows rows only)
+  int gather_k;
+  uint64_t gather_magic;     // slot_div_magic(gather_k)
   const uint16_t* a_shared;  // [rows_shared, K] (nullptr: rows follow the routed rows)
   int64_t lda;
   const int32_t* offsets;  // [E+1], device
@@ -270,19 +274,79 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
   const uint16_t* c_b0 = nullptr;  // B operand base(s)
   const uint16_t* c_b1 = nullptr;
   int c_last_row = 0, c_n0 = 0;    // last valid A row of the tile, first B row
+  // GATEUP_FWD: this lane's byte offsets (from c_a) of its A rows of the tile,
+  // rows 64 i + drow clamped to the last valid one.  With args.gather the
+  // routed rows are token rows of x (row r: x row gather[r] / gather_k); the
+  // lane's four indices of an item are loaded when the item before it is set
+  // up (g_pf, vector loads issued after that stage's copies, complete by the
+  // next stage's wait) and consumed one item later.
+  uint32_t a_off[LA];
+  int32_t g_pf[LA] = {0, 0, 0, 0};
+  bool g_pf_routed = false;  // the prefetched item is a routed tile (its rows are gathered)
+  auto item_rows = [&](int ti, int& row0, int& last, bool& routed) {
+    int tile, k0_, kn_, slot;
+    split_item(sp, nk, b + ti * NP, tile, k0_, kn_, slot);
+    int g, tm, tn, row_base, M;
+    routed = locate_tile(args, offsets, tiles_n, tile, g, tm, tn, row_base, M) && g < args.E;
+    row0 = row_base + tm * BM;
+    last = min(M - tm * BM, BM) - 1;
+  };
+  auto prefetch_rows = [&](int ti) {
+    // item ti's indices (no loads past the last item or for the shared group)
+    g_pf_routed = false;
+    if (ti >= my_items) return;
+    int row0, last;
+    item_rows(ti, row0, last, g_pf_routed);
+    if (!g_pf_routed) return;
+#pragma unroll
+    for (int i = 0; i < LA; ++i) {
+      const uint32_t off = static_cast<uint32_t>(row0 + min(64 * i + drow, last)) * 4u;
+      asm volatile("global_load_dword %0, %1, %2" : "+v"(g_pf[i]) : "v"(off), "s"(args.gather) : "memory");
+    }
+  };
   auto copy_tile = [&](int ti) {
     int tile, slot;
     split_item(sp, nk, b + ti * NP, tile, c_k0, c_kn, slot);
     int g, tm, tn, row_base, M;
     locate_tile(args, offsets, tiles_n, tile, g, tm, tn, row_base, M);
-    const uint16_t* A = (g < args.E || args.a_shared == nullptr) ? args.a_routed + static_cast<int64_t>(row_base) * args.lda
-                                                                 : args.a_shared;
-    c_a = A + static_cast<int64_t>(tm) * BM * args.lda;
+    const bool gathered = MODE == GATEUP_FWD && args.gather != nullptr && g < args.E;
+    const uint16_t* A = gathered ? args.a_routed
+                        : (g < args.E || args.a_shared == nullptr) ? args.a_routed + static_cast<int64_t>(row_base) * args.lda
+                                                                   : args.a_shared;
+    c_a = gathered ? A : A + static_cast<int64_t>(tm) * BM * args.lda;
     c_last_row = min(M - tm * BM, BM) - 1;
     c_b0 = args.b0[g];
     c_b1 = args.b1[g];
     c_n0 = tn * TN_COLS;
+    if constexpr (MODE == GATEUP_FWD) {
+      if (gathered) {
+        // g_pf holds this item's indices (loaded one item ahead, a stage wait
+        // has normally passed since; the wait here covers every operation older
+        // than this stage's LT copies and orders the use after it)
+        asm volatile("s_waitcnt vmcnt(%4)"
+                     : "+v"(g_pf[0]), "+v"(g_pf[1]), "+v"(g_pf[2]), "+v"(g_pf[3])
+                     : "n"(LT)
+                     : "memory");
+#pragma unroll
+        for (int i = 0; i < LA; ++i) {
+          const uint32_t tok = slot_token(static_cast<uint32_t>(g_pf[i]), args.gather_magic);
+          a_off[i] = (tok * static_cast<uint32_t>(args.lda) + static_cast<uint32_t>(dchunk * 8)) * 2u;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < LA; ++i)
+          a_off[i] = static_cast<uint32_t>(min(64 * i + drow, c_last_row) * static_cast<int>(args.lda) + dchunk * 8) * 2u;
+      }
+      if (args.gather != nullptr) prefetch_rows(ti + 1);
+    }
   };
+  if constexpr (MODE == GATEUP_FWD) {
+    if (args.gather != nullptr) {
+      // the first item's indices, waited for at once
+      prefetch_rows(0);
+      asm volatile("s_waitcnt vmcnt(0)" : "+v"(g_pf[0]), "+v"(g_pf[1]), "+v"(g_pf[2]), "+v"(g_pf[3])::"memory");
+    }
+  }
   copy_tile(0);
   const int lda = static_cast<int>(args.lda), ldb = static_cast<int>(args.ldb);
   auto issue = [&](int it) {
@@ -290,8 +354,12 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
     const int kofs = (c_k0 + c_kt) * BK;
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
-      const int r = min(64 * i + drow, c_last_row);
-      copy16(st + i * 8192, c_a + kofs, static_cast<uint32_t>(r * lda + dchunk * 8) * 2u);
+      if constexpr (MODE == GATEUP_FWD) {
+        copy16(st + i * 8192, c_a + kofs, a_off[i]);
+      } else {
+        const int r = min(64 * i + drow, c_last_row);
+        copy16(st + i * 8192, c_a + kofs, static_cast<uint32_t>(r * lda + dchunk * 8) * 2u);
+      }
     }
     if constexpr (BTR) {
       // 64 k rows of 512 bytes: instruction i of wave w writes k rows 16 i + 2 w, +1;
@@ -921,9 +989,12 @@ struct WgradArgs {
   const uint16_t* a_routed;
   const uint16_t* a_shared;
   int64_t lda;
-  const uint16_t* b_routed;
+  const uint16_t* b_routed;  // [rows_routed, n_out], or with b_gather: x [T, n_out]
   const uint16_t* b_shared;
   int64_t ldb;
+  const int32_t* b_gather;   // routed row r of B is b_routed row b_gather[r] / gather_k (nullptr: row r)
+  int gather_k;
+  uint64_t gather_magic;     // slot_div_magic(gather_k)
   const int32_t* offsets;
   int E;
   int rows_routed;
@@ -978,6 +1049,11 @@ __global__ __launch_bounds__(core::NT, 1) void wgrad_tr_kernel(const WgradArgs a
                                                                const int32_t* __restrict__ offsets) {
   using namespace core;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+  // Gathered B rows: the slot indices of each stage's 64 k rows (ring of eight
+  // stages, filled by global -> LDS copies three stages ahead and read one
+  // stage ahead, after the stage waits that cover them; a slot is refilled
+  // four stages after its last read, with stage barriers in between).
+  __shared__ int32_t idx_ring[8][BK];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = w / WN, wn = w % WN;  // wave block: 64 m x 128 n
@@ -1029,9 +1105,20 @@ __global__ __launch_bounds__(core::NT, 1) void wgrad_tr_kernel(const WgradArgs a
   const int nk = (k_end - k_begin + BK - 1) / BK;
   const bool shared_sep = (g >= args.E);
   const uint16_t* A = (shared_sep && args.a_shared) ? args.a_shared : args.a_routed + static_cast<int64_t>(row_base) * args.lda;
-  const uint16_t* B = (shared_sep && args.b_shared) ? args.b_shared : args.b_routed + static_cast<int64_t>(row_base) * args.ldb;
+  const bool gathered = args.b_gather != nullptr && !shared_sep;
+  const uint16_t* B = (shared_sep && args.b_shared) ? args.b_shared
+                      : gathered ? args.b_routed
+                                 : args.b_routed + static_cast<int64_t>(row_base) * args.ldb;
   const int lda = static_cast<int>(args.lda), ldb = static_cast<int>(args.ldb);
-
+  const uint32_t ring = lds_addr(&idx_ring[0][0]);
+  // stage kt's slot indices into ring slot kt % 8 (wave 0; rows past k_end
+  // repeat the last valid one)
+  auto fetch_idx = [&](int kt) {
+    if (w == 0) {
+      const int r = min(k_begin + kt * BK + lane, k_end - 1);
+      copy4(ring + (kt & 7) * (BK * 4), args.b_gather + row_base, static_cast<uint32_t>(r) * 4u);
+    }
+  };
   // ---- copies: instruction i of wave w writes k rows 16 i + drow (1 KB = 2 rows of 512 B);
   // lane chunk p = l % 32 holds logical chunk c of the row
   const int drow = 2 * w + (lane >> 5);
@@ -1039,6 +1126,22 @@ __global__ __launch_bounds__(core::NT, 1) void wgrad_tr_kernel(const WgradArgs a
   const int c = (((p >> 1) ^ wsw(drow)) << 1) | (p & 1);  // wsw(16 i + drow) == wsw(drow)
   const int colA = min(m0 + 8 * c, args.m_out - 8), colB = min(n0 + 8 * c, args.n_out - 8);
   const uint32_t lds_copy = sbase + w * 1024;
+  uint32_t b_off[4];  // gathered B: this lane's byte offsets (from B) of its 4 k rows of a coming stage
+  auto form_offsets = [&](int kt) {
+    const int last = k_end - 1 - (k_begin + kt * BK);  // >= 0 for kt < nk
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = min(16 * i + drow, last);
+      const uint32_t tok = slot_token(static_cast<uint32_t>(idx_ring[kt & 7][r]), args.gather_magic);
+      b_off[i] = (tok * static_cast<uint32_t>(ldb) + static_cast<uint32_t>(colB)) * 2u;
+    }
+  };
+  if (gathered) {
+    // stages 0..2 before the first copies (issue(kt) fetches stage kt + 3)
+    for (int q = 0; q < 3 && q < nk; ++q) fetch_idx(q);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  }
+
   auto issue = [&](int kt) {
     const int k0 = k_begin + kt * BK;
     const int last = k_end - 1 - k0;  // last valid k row of this stage
@@ -1048,10 +1151,20 @@ __global__ __launch_bounds__(core::NT, 1) void wgrad_tr_kernel(const WgradArgs a
       const int r = min(16 * i + drow, last);
       copy16(st + i * 8192, A + static_cast<int64_t>(k0) * lda, static_cast<uint32_t>(r * lda + colA) * 2u);
     }
+    if (gathered) {
+      // k row r of the stage is x row (slot of group row k0 + r) / k, at the
+      // offsets b_off formed from the stage's ring slot (at the end of the K
+      // step before, or before the first copies)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = min(16 * i + drow, last);
-      copy16(st + A_BYTES + i * 8192, B + static_cast<int64_t>(k0) * ldb, static_cast<uint32_t>(r * ldb + colB) * 2u);
+      for (int i = 0; i < 4; ++i) copy16(st + A_BYTES + i * 8192, B, b_off[i]);
+      if (kt + 3 < nk) fetch_idx(kt + 3);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = min(16 * i + drow, last);
+        copy16(st + A_BYTES + i * 8192, B + static_cast<int64_t>(k0) * ldb,
+               static_cast<uint32_t>(r * ldb + colB) * 2u);
+      }
     }
   };
   // Rows past k_end in a stage hold copies of the last valid row: zero their A
@@ -1077,8 +1190,13 @@ __global__ __launch_bounds__(core::NT, 1) void wgrad_tr_kernel(const WgradArgs a
   const uint32_t xa = static_cast<uint32_t>((8 * h + jq) * 512 + (((4 * wm) ^ fr) << 5) + 8 * q);
   const uint32_t xb = static_cast<uint32_t>(A_BYTES + (8 * h + jq) * 512 + ((8 * wn + fr) << 5) + 8 * q);
 
+  if (gathered) form_offsets(0);
   issue(0);
-  if (nk > 1) issue(1);
+  if (nk > 1) {
+    if (gathered) form_offsets(1);
+    issue(1);
+  }
+  if (gathered) form_offsets(min(2, nk - 1));
   sync_stage(0, nk > 1);
 
   f32x4 acc[FM][FN];
@@ -1129,6 +1247,12 @@ __global__ __launch_bounds__(core::NT, 1) void wgrad_tr_kernel(const WgradArgs a
 #pragma unroll
       for (int f = 0; f < FN; ++f) fb[f] = nb[f];
     }
+    // gathered B: the offsets of stage kt + 3 (issued in the next K step),
+    // formed after this step's MFMAs rather than right after a barrier,
+    // where every wave would wait for its ring reads at once.  The ring slot
+    // landed before this step's second wait; past the last stage the last
+    // one is formed again (unused).
+    if (gathered) form_offsets(min(kt + 3, nk - 1));
   }
 
   // ---- epilogue: lane holds C[m0 + 64 wm + 16 i + l % 16][n0 + 128 wn + 16 j + 4 (l / 16) + 0..3]
@@ -1316,7 +1440,8 @@ extern "C" size_t fmoe_split_workspace_bytes(void) {
   return P * core::BM * core::BN * sizeof(float) + (P + 1) * 16;  // partials + descriptors
 }
 
-extern "C" int fmoe_gateup_fwd(const void* x_routed, const void* x_shared, const int32_t* offsets,
+extern "C" int fmoe_gateup_fwd(const void* x_routed, const int32_t* gather, int gather_k, int64_t gather_tokens,
+                               const void* x_shared, const int32_t* offsets,
                                int n_experts, int64_t rows_routed, int64_t rows_shared, int64_t dim,
                                int64_t inter, const void* const* w1, const void* const* w3,
                                void* ab, void* h, void* workspace, size_t workspace_bytes, void* stream) {
@@ -1327,8 +1452,19 @@ extern "C" int fmoe_gateup_fwd(const void* x_routed, const void* x_shared, const
       (rows_shared && !x_shared))
     return FMOE_ERR_INVALID_ARG;
   if (!aligned16(ab) || !aligned16(h)) return FMOE_ERR_ALIGN;
+  if (gather) {
+    // routed row r reads x_routed ([gather_tokens, dim]) row gather[r] / gather_k;
+    // the tiled kernel reads the indices in windows of 8 and forms 32-bit offsets
+    if (gather_k <= 0 || gather_k > FMOE_MAX_TOPK || gather_tokens <= 0 || rows_routed < 8 ||
+        rows_routed + rows_shared <= kSmallLaunchRows || gather_tokens * dim * 2 >= (int64_t(1) << 31) ||
+        rows_routed >= (int64_t(1) << 29))
+      return FMOE_ERR_SHAPE;
+  }
   GemmArgs a = {};
   a.a_routed = static_cast<const uint16_t*>(x_routed);
+  a.gather = gather;
+  a.gather_k = gather ? gather_k : 1;
+  a.gather_magic = slot_div_magic(a.gather_k);
   a.a_shared = static_cast<const uint16_t*>(x_shared);
   a.lda = dim;
   fill_groups(a, offsets, n_experts, rows_routed, rows_shared);
@@ -1470,6 +1606,7 @@ extern "C" size_t fmoe_weight_grad_workspace_bytes(int64_t rows_routed, int64_t 
 
 extern "C" int fmoe_weight_grad(const void* a_routed, const void* a_shared, int64_t lda,
                                 const void* b_routed, const void* b_shared, int64_t ldb,
+                                const int32_t* b_gather, int gather_k, int64_t gather_tokens,
                                 const int32_t* offsets, int n_experts, int64_t rows_routed,
                                 int64_t rows_shared, int64_t m_out, int64_t n_out, int64_t m_split,
                                 void* const* out_lo, void* const* out_hi, int out_dtype,
@@ -1492,6 +1629,15 @@ extern "C" int fmoe_weight_grad(const void* a_routed, const void* a_shared, int6
   a.b_routed = static_cast<const uint16_t*>(b_routed);
   a.b_shared = static_cast<const uint16_t*>(b_shared);
   a.ldb = ldb;
+  if (b_gather) {
+    // routed row r of B is b_routed ([gather_tokens, n_out]) row b_gather[r] / gather_k
+    if (gather_k <= 0 || gather_k > FMOE_MAX_TOPK || gather_tokens <= 0 ||
+        gather_tokens * ldb * 2 >= (int64_t(1) << 31) || rows_routed >= (int64_t(1) << 29))
+      return FMOE_ERR_SHAPE;
+  }
+  a.b_gather = b_gather;
+  a.gather_k = b_gather ? gather_k : 1;
+  a.gather_magic = slot_div_magic(a.gather_k);
   a.offsets = offsets;
   a.E = n_experts;
   a.rows_routed = static_cast<int>(rows_routed);

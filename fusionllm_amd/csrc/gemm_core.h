@@ -70,6 +70,20 @@ __device__ __forceinline__ int2 sload2(const int32_t* p) {
   return v;
 }
 
+// Scalar load of eight consecutive ints at a wave-uniform address (tracked by
+// lgkmcnt, waited for at once, as sload2).
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ i32x8 sload8(const int32_t* p) {
+  i32x8 v;
+  asm volatile("s_load_dwordx8 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)\n" : "=s"(v) : "s"(p) : "memory");
+  return v;
+}
+
+// One 4-byte-per-lane copy global -> LDS (lane l writes LDS bytes lds + 4 l).
+__device__ __forceinline__ void copy4(uint32_t lds, const void* base, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2\n" ::"s"(lds), "v"(voff), "s"(base) : "memory");
+}
+
 // Wait until at most N vector-memory operations of this wave are in flight and
 // its LDS reads are done, then synchronise the workgroup.
 template <int N>

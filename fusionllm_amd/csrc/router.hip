@@ -439,9 +439,9 @@ __device__ __forceinline__ float slot_dlogit(const float* __restrict__ dwt, cons
 }
 
 // Gate weight/bias gradient as a segmented column reduction over the
-// expert-contiguous rows:  dWg[e] = sum_{r in e} dl_row[r] * x_perm[r],
+// expert-contiguous rows:  dWg[e] = sum_{r in e} dl_row[r] * x[perm[r] / k],
 // dbg[e] = sum_{r in e} dl_row[r], where dl_row[r] is the logit gradient of
-// slot perm[r].  Expert e's rows are cut into ceil(M_e / kChunkRows) chunks,
+// slot perm[r] (row r's token rows are read from x through perm).  Expert e's rows are cut into ceil(M_e / kChunkRows) chunks,
 // numbered consecutively over the experts (chunk_base(e) = sum of the chunk
 // counts of experts < e).  Stage 1: one block per chunk reads the E + 1
 // offsets once (into LDS), issues its first kPartialBatch row loads, forms
@@ -458,9 +458,10 @@ constexpr int kPartialThreads = 128;
 __global__ __launch_bounds__(kPartialThreads) void router_wgrad_partial_kernel(
     const float* __restrict__ dw, const float* __restrict__ v, const int32_t* __restrict__ perm, int k,
     float rs, float* __restrict__ dl, const int32_t* __restrict__ offsets, int E,
-    const uint16_t* __restrict__ x_perm, int dim, float* __restrict__ partial) {
+    const uint16_t* __restrict__ x, int dim, float* __restrict__ partial) {
   __shared__ int off_sh[FMOE_MAX_EXPERTS + 1];
   __shared__ float gsh[kChunkRows];
+  __shared__ int tok_sh[kChunkRows];  // token of each row of the chunk (perm[r] / k)
   if (threadIdx.x <= E) off_sh[threadIdx.x] = offsets[threadIdx.x];  // one load for all E + 1
   __syncthreads();
   int c = blockIdx.x, e = 0;
@@ -475,12 +476,20 @@ __global__ __launch_bounds__(kPartialThreads) void router_wgrad_partial_kernel(
   float* out = partial + static_cast<int64_t>(blockIdx.x) * (dim + 1);
   const int nchunk8 = dim / 8;
   const int64_t ld = dim / 8;
+  // The chunk's rows are token rows of x: row r is token perm[r] / k (rows
+  // past r1 repeat row r1 - 1).
+  int my_slot = 0;
+  if (threadIdx.x < kChunkRows) {
+    my_slot = perm[min(r0 + static_cast<int>(threadIdx.x), r1 - 1)];
+    tok_sh[threadIdx.x] = my_slot / k;
+  }
+  __syncthreads();
   // Column passes of kPartialThreads columns (the same count for every
   // thread, so the barrier in the first pass is reached by all).
   for (int cb = 0; cb <= nchunk8; cb += kPartialThreads) {
     const int col8 = cb + threadIdx.x;
     const bool is_col = col8 < nchunk8;
-    const uint4* xc = reinterpret_cast<const uint4*>(x_perm) + (is_col ? col8 : 0);
+    const uint4* xc = reinterpret_cast<const uint4*>(x) + (is_col ? col8 : 0);
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     // Batches of kPartialBatch rows: every load first (rows past r1 read row
     // r1 - 1, in bounds), then the rows below r1 added in order through a
@@ -489,12 +498,12 @@ __global__ __launch_bounds__(kPartialThreads) void router_wgrad_partial_kernel(
     uint4 xv[kPartialBatch];
     auto load_batch = [&](int rb) {
 #pragma unroll
-      for (int u = 0; u < kPartialBatch; ++u) xv[u] = xc[static_cast<int64_t>(min(rb + u, r1 - 1)) * ld];
+      for (int u = 0; u < kPartialBatch; ++u) xv[u] = xc[static_cast<int64_t>(tok_sh[min(rb + u, r1 - 1) - r0]) * ld];
     };
     if (is_col) load_batch(r0);
     if (cb == 0) {
       if (threadIdx.x < r1 - r0) {
-        const int slot = perm[r0 + threadIdx.x];
+        const int slot = my_slot;
         const int t = slot / k, jr = slot - t * k;
         const float g = slot_dlogit(dw + static_cast<int64_t>(t) * k, v + static_cast<int64_t>(t) * k, k, jr, rs);
         dl[slot] = g;
@@ -713,7 +722,7 @@ extern "C" size_t fmoe_router_bwd_workspace_bytes(int64_t T, int64_t dim, int n_
 }
 
 extern "C" int fmoe_router_bwd(const float* d_weights, const float* topv, const int32_t* perm,
-                               const int32_t* offsets, const void* x_perm, int64_t T, int64_t dim,
+                               const int32_t* offsets, const void* x, int64_t T, int64_t dim,
                                int n_experts, int k, float route_scale, float* d_logits,
                                void* d_gate_w, void* d_gate_b, int grad_dtype, void* workspace,
                                size_t workspace_bytes, void* stream) {
@@ -730,17 +739,17 @@ extern "C" int fmoe_router_bwd(const float* d_weights, const float* topv, const 
                                                                   n_experts, (int)dim, grad_dtype);
     return launch_status();
   }
-  if (!d_weights || !topv || !perm || !offsets || !x_perm || !d_logits || !d_gate_w || !d_gate_b ||
+  if (!d_weights || !topv || !perm || !offsets || !x || !d_logits || !d_gate_w || !d_gate_b ||
       !workspace)
     return FMOE_ERR_INVALID_ARG;
   if (workspace_bytes < fmoe_router_bwd_workspace_bytes(T, dim, n_experts, k))
     return FMOE_ERR_WORKSPACE;
-  if (!aligned16(x_perm)) return FMOE_ERR_ALIGN;
+  if (!aligned16(x)) return FMOE_ERR_ALIGN;
   const int64_t max_chunks = router_max_chunks(T, n_experts, k);
   float* partial = static_cast<float*>(workspace);
   router_wgrad_partial_kernel<<<dim3(max_chunks), dim3(128), 0, s>>>(
       d_weights, topv, perm, k, route_scale, d_logits, offsets, n_experts,
-      static_cast<const uint16_t*>(x_perm), (int)dim, partial);
+      static_cast<const uint16_t*>(x), (int)dim, partial);
   router_wgrad_final_kernel<<<dim3(ceil_div(dim + 1, 16), n_experts), dim3(256), 0, s>>>(
       partial, offsets, n_experts, (int)dim, grad_dtype, d_gate_w, d_gate_b);
   return launch_status();

@@ -218,6 +218,26 @@ class DenseFFN(SwiGLUExpert):
     one-group kernels."""
 
 
+# Whether the training forward reads the routed token rows of x through the
+# dispatch's permutation in the tiled products (gate/up forward, dW1|dW3)
+# instead of writing the gathered copy x_perm.  Measured on one MI355X at C2
+# (16384 tokens, both variants in one session): dropping the copy saves 11 us
+# in the dispatch, but the gate/up forward reading rows through perm takes
+# 9-14 us longer and dW1|dW3 18-21 us longer (scattered 128-byte row pieces
+# instead of consecutive rows), so the block keeps x_perm.  The entry points
+# keep the option (fmoe_gateup_fwd, fmoe_weight_grad): it saves T*k*dim*2
+# bytes of HBM.
+GATHER_ROWS = False
+
+
+def gathers_rows(T: int, k: int, has_shared: bool) -> bool:
+    """Whether the block reads the routed token rows of x through perm (no
+    x_perm): only with GATHER_ROWS, and only for launches of more than
+    SMALL_LAUNCH_ROWS rows (the tiled products; the small-group kernels read
+    x_perm)."""
+    return GATHER_ROWS and T * k >= 8 and T * k + (T if has_shared else 0) > K.SMALL_LAUNCH_ROWS
+
+
 def _forward_pass(meta, x, gate_w, gate_b, weights, residual=None, counts_host=None):
     """The forward kernels of DeepSeekMoE.forward (models/moe.py:79-87); returns
     the output and every intermediate the backward pass needs.  With a
@@ -230,6 +250,7 @@ def _forward_pass(meta, x, gate_w, gate_b, weights, residual=None, counts_host=N
     xb, gwb, gbb, *wb = _bf16_operands([x, gate_w, gate_b, *weights])
     G = E + (1 if has_shared else 0)
     w1s, w3s, w2s = wb[0::3][:G], wb[1::3][:G], wb[2::3][:G]
+    gather = gathers_rows(T, k, has_shared)
 
     if 0 < T <= K.TINY_BATCH and T * E <= 64 and d <= 2048:
         # decode-sized: routing and dispatch in one launch (one workgroup)
@@ -240,15 +261,17 @@ def _forward_pass(meta, x, gate_w, gate_b, weights, residual=None, counts_host=N
         # one-launch small dispatch below are faster (C3 replay at 32 tokens: 49 against 55 us).
         # The expert counts reach counts_host from the kernel itself.
         idx, idx64, w, v, counts, offsets, perm, pos, x_perm = K.route_and_dispatch(
-            xb, gwb, gbb, k, rs, counts_host=counts_host)
+            xb, gwb, gbb, k, rs, gather=not gather, counts_host=counts_host)
         counts_host = None
     else:
         idx, idx64, w, v = K.router_fwd(xb, gwb, gbb, k, rs)
-        counts, offsets, perm, pos, x_perm = K.dispatch(idx, xb, E)
+        counts, offsets, perm, pos, x_perm = K.dispatch(idx, xb, E, gather=not gather)
     if counts_host is not None:
         counts_host.copy_(counts, non_blocking=True)
     rows_r, rows_s = T * k, (T if has_shared else 0)
-    ab, h = K.gateup_fwd(x_perm, xb if has_shared else None, offsets, E, w1s, w3s, inter)
+    # routed rows: token rows of x through perm (gather), or the gathered copy x_perm
+    ab, h = K.gateup_fwd(xb if gather else x_perm, xb if has_shared else None, offsets, E, w1s, w3s, inter,
+                         gather=perm if gather else None, k=k)
     o = K.down_fwd(h, offsets, E, rows_r, rows_s, w2s, d)
     y = K.combine_fwd(o, idx, w, pos, rows_r, has_shared, out_dtype, residual)
     return xb, gwb, wb, idx, idx64, w, v, counts, offsets, perm, pos, x_perm, ab, h, o, y
@@ -323,10 +346,11 @@ def _backward_pass(ctx, saved, dy):
     dx_rows = K.gateup_bwd_dx(d_ab, offsets, E, rows_r, rows_s, w1s, w3s, d)
     dw1 = [torch.empty(inter, d, dtype=w_dtypes[3 * g], device=xb.device) for g in range(G)]
     dw3 = [torch.empty(inter, d, dtype=w_dtypes[3 * g + 1], device=xb.device) for g in range(G)]
-    K.weight_grad(d_ab, None, x_perm, xb if has_shared else None, offsets, E, rows_r, rows_s,
-                  inter, dw1, dw3, w_dtypes[0], tag="w13")
+    gather = x_perm is None or (x_perm.shape[0] == 0 and rows_r > 0)
+    K.weight_grad(d_ab, None, xb if gather else x_perm, xb if has_shared else None, offsets, E, rows_r, rows_s,
+                  inter, dw1, dw3, w_dtypes[0], b_gather=perm if gather else None, k=k, tag="w13")
     # Router: logits gradient, gate weight/bias gradient.
-    d_logits, dgw, dgb = K.router_bwd(d_w, v, perm, offsets, x_perm, E, rs, gw_dtype)
+    d_logits, dgw, dgb = K.router_bwd(d_w, v, perm, offsets, xb, E, rs, gw_dtype)
     if dgb.dtype != gb_dtype:
         dgb = dgb.to(gb_dtype)
 

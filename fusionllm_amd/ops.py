@@ -15,7 +15,8 @@ no tokens get zero gradients instead of None.
 moe_fwd outputs: y [T,d] (out_dtype), indices [T,k] int64, weights [T,k]
 fp32, counts [E] int32, then the tensors the backward reads: idx32 [T,k],
 topv [T,k] fp32, offsets [E+1], perm [T*k], pos_of_slot [T*k], x_perm
-[T*k,d] bf16, ab [rows,2I] bf16, h [rows,I] bf16, o [rows,d] bf16.
+[T*k,d] bf16 (0 rows when the routed rows are read from x through perm),
+ab [rows,2I] bf16, h [rows,I] bf16, o [rows,d] bf16.
 moe_bwd returns [dx, d_gate_w, d_gate_b, *d_weights] in the inputs' dtypes.
 
 ``fusionllm::swiglu_fwd`` / ``swiglu_bwd`` do the same for the dense SwiGLU
@@ -31,7 +32,7 @@ import torch
 from torch import Tensor
 
 from . import _kernels as K
-from .moe import _backward_pass, _bf16_operands, _dense_backward, _dense_offsets, _forward_pass
+from .moe import _backward_pass, _bf16_operands, _dense_backward, _dense_offsets, _forward_pass, gathers_rows
 
 
 def _meta(gate_w: Tensor, weights: list[Tensor], k: int, route_scale: float, has_shared: bool,
@@ -47,6 +48,8 @@ def moe_fwd(x: Tensor, gate_w: Tensor, gate_b: Tensor, weights: list[Tensor], k:
     meta = _meta(gate_w, weights, k, route_scale, has_shared, out_dtype)
     fw = _forward_pass(meta, x, gate_w, gate_b, weights)
     xb, gwb, wb, idx, idx64, w, v, counts, offsets, perm, pos, x_perm, ab, h, o, y = fw
+    if x_perm is None:  # routed rows read through perm: no gathered copy (0 rows)
+        x_perm = xb.new_empty((0, xb.shape[1]))
     return y, idx64, w, counts, idx, v, offsets, perm, pos, x_perm, ab, h, o
 
 
@@ -57,9 +60,10 @@ def _(x, gate_w, gate_b, weights, k, route_scale, has_shared, out_dtype):
     rows = T * k + (T if has_shared else 0)
     i32, f32, bf = torch.int32, torch.float32, torch.bfloat16
     e = lambda *shape, dtype: x.new_empty(shape, dtype=dtype)
+    xp_rows = 0 if gathers_rows(T, k, has_shared) else T * k
     return (e(T, d, dtype=out_dtype), e(T, k, dtype=torch.int64), e(T, k, dtype=f32), e(E, dtype=i32),
             e(T, k, dtype=i32), e(T, k, dtype=f32), e(E + 1, dtype=i32), e(T * k, dtype=i32),
-            e(T * k, dtype=i32), e(T * k, d, dtype=bf), e(rows, 2 * inter, dtype=bf), e(rows, inter, dtype=bf),
+            e(T * k, dtype=i32), e(xp_rows, d, dtype=bf), e(rows, 2 * inter, dtype=bf), e(rows, inter, dtype=bf),
             e(rows, d, dtype=bf))
 
 

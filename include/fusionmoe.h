@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define FMOE_ABI_VERSION 12
+#define FMOE_ABI_VERSION 13
 #define FMOE_MAX_EXPERTS 64
 #define FMOE_MAX_TOPK 8
 #define FMOE_MAX_CAST 64
@@ -159,12 +159,18 @@ int fmoe_route_and_dispatch(const void* x, const void* gate_w, const void* gate_
  * for the shared expert (moe.py:86), as one launch.
  *   a = x_e w1_e^T, b = x_e w3_e^T (bf16-rounded, as nn.Linear returns),
  *   h = bf16(bf16(silu(a)) * b).
- * x_routed: [rows_routed, dim] (x_perm from fmoe_dispatch); x_shared: [T, dim].
+ * x_routed: [rows_routed, dim] (x_perm from fmoe_dispatch), or, with gather
+ * non-null, the token rows x [gather_tokens, dim]: routed row r then reads
+ * x row gather[r] / gather_k (gather = perm from the dispatch; rows_routed
+ * >= 8, rows_routed + rows_shared > 4096 (decode-sized launches take x_perm),
+ * gather_tokens * dim * 2 < 2^31), so no gathered copy of x is needed
+ * (the reference's x[token_ids], moe.py:75); x_shared: [T, dim].
  * Outputs over all rows: ab [rows, 2*inter] (a in columns 0..inter-1, b in
  * inter..2*inter-1; kept for the backward pass), h [rows, inter].
  * workspace: see fmoe_split_workspace_bytes.
  * ------------------------------------------------------------------------- */
-int fmoe_gateup_fwd(const void* x_routed, const void* x_shared,
+int fmoe_gateup_fwd(const void* x_routed, const int32_t* gather, int gather_k,
+                    int64_t gather_tokens, const void* x_shared,
                     const int32_t* offsets, int n_experts,
                     int64_t rows_routed, int64_t rows_shared,
                     int64_t dim, int64_t inter,
@@ -257,7 +263,9 @@ int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int n_experts,
  * Row i < m_split of G_e goes to out_lo[e] ([m_split, n_out]); rows >= m_split
  * go to out_hi[e] ([m_out - m_split, n_out]).  out dtype bf16 or f32.
  * For w2: A = d_out, B = h, m_split = m_out = dim.  For w1/w3: A = d_ab,
- * B = x, m_split = inter (out_lo = dw1, out_hi = dw3).
+ * B = x, m_split = inter (out_lo = dw1, out_hi = dw3).  With b_gather
+ * non-null, b_routed is the token rows x [gather_tokens, n_out] and routed
+ * row r of B is x row b_gather[r] / gather_k (gather_tokens * ldb * 2 < 2^31).
  * The reduction over rows is split into fixed chunks summed in chunk order,
  * so the result is deterministic.  Experts with no rows get a zero G_e
  * (the module still reports None for them, as the reference leaves their
@@ -267,6 +275,7 @@ size_t fmoe_weight_grad_workspace_bytes(int64_t rows_routed, int64_t rows_shared
                                         int n_experts, int64_t m_out, int64_t n_out);
 int fmoe_weight_grad(const void* a_routed, const void* a_shared, int64_t lda,
                      const void* b_routed, const void* b_shared, int64_t ldb,
+                     const int32_t* b_gather, int gather_k, int64_t gather_tokens,
                      const int32_t* offsets, int n_experts,
                      int64_t rows_routed, int64_t rows_shared,
                      int64_t m_out, int64_t n_out, int64_t m_split,
@@ -278,13 +287,14 @@ int fmoe_weight_grad(const void* a_routed, const void* a_shared, int64_t lda,
  * top-k scatter, sigmoid backward, then the gate Linear's weight and bias
  * gradients.  d_logits [T,k] fp32 holds dL/dlogit for each selected expert
  * (the other logits get zero gradient); d_gate_w [E, dim] and d_gate_b [E]
- * are written in grad_dtype.  The reductions over tokens run over x_perm in
- * expert-contiguous order with a fixed chunking: deterministic.
+ * are written in grad_dtype.  The reductions over tokens run over the routed
+ * rows in expert-contiguous order with a fixed chunking (deterministic); the
+ * row r reads token row x[perm[r] / k] ([T, dim] bf16, 16-byte aligned).
  * ------------------------------------------------------------------------- */
 size_t fmoe_router_bwd_workspace_bytes(int64_t T, int64_t dim, int n_experts, int k);
 int fmoe_router_bwd(const float* d_weights, const float* topv,
                     const int32_t* perm, const int32_t* offsets,
-                    const void* x_perm, int64_t T, int64_t dim,
+                    const void* x, int64_t T, int64_t dim,
                     int n_experts, int k, float route_scale,
                     float* d_logits, void* d_gate_w, void* d_gate_b,
                     int grad_dtype, void* workspace, size_t workspace_bytes,

@@ -206,7 +206,7 @@ def test_router_bwd(gpu_device, T, d, E, k, gdt, empty):
     counts, offsets, perm, pos, x_perm = K.dispatch(idx, xd, E)
     g = torch.Generator().manual_seed(5)
     d_w = torch.randn(T, k, generator=g).float()
-    d_logits, dgw, dgb = K.router_bwd(d_w.to(gpu_device), v, perm, offsets, x_perm, E, rs, gdt)
+    d_logits, dgw, dgb = K.router_bwd(d_w.to(gpu_device), v, perm, offsets, xd, E, rs, gdt)
     ref_dl = mo.router_dlogits(d_w.numpy(), v.cpu().numpy(), rs)
     assert torch.equal(f32_bits(d_logits.cpu()), f32_bits(torch.from_numpy(ref_dl)))
     dl64 = torch.from_numpy(ref_dl).double().reshape(-1)
@@ -421,6 +421,54 @@ def test_backward_products(gpu_device, counts, shared, d, I):
         assert rel_l2(dw3[grp].cpu(), dw3_ref) < 1e-5
 
 
+@pytest.mark.parametrize("T,d,I,E,k,bias", [(3000, 768, 2048, 8, 2, "skew"), (2400, 256, 320, 16, 3, "spread"),
+                                              (4500, 192, 128, 4, 1, "tiny_last")])
+def test_gathered_rows_match_the_gathered_copy(gpu_device, T, d, I, E, k, bias):
+    # Launches of more than 4096 rows can read the routed token rows of x
+    # through the dispatch's permutation (routed row r = x row perm[r] // k)
+    # instead of a gathered copy x_perm: gate/up forward and the w1 / w3 weight
+    # gradient bit-identical to the same products over x_perm (the same values reach
+    # the same MFMAs), for skewed groups, partial tiles and a last expert with
+    # fewer than 8 rows (the index windows' clamp at the end of perm).
+    D = gpu_device
+    g = torch.Generator().manual_seed(T + E)
+    x = _bf(T, d, g=g).to(D)
+    gw = _bf(E, d, scale=0.05, g=g).to(D)
+    gb = torch.zeros(E)
+    if bias == "skew":
+        gb[:2] = 1.5
+    elif bias == "tiny_last":
+        gb[E - 1] = -2.5  # the last expert gets only a few tokens
+    idx, _, _, _ = K.router_fwd(x, gw, gb.bfloat16().to(D), k, 1.0)
+    counts, offsets, perm, pos, x_perm = K.dispatch(idx, x, E)
+    if bias == "tiny_last":
+        assert 0 < int(counts[E - 1]) < 8
+    G = E + 1
+    w1 = [_bf(I, d, scale=0.05, g=g).to(D) for _ in range(G)]
+    w3 = [_bf(I, d, scale=0.05, g=g).to(D) for _ in range(G)]
+    rows_r = T * k
+    ab0, h0 = K.gateup_fwd(x_perm, x, offsets, E, w1, w3, I)
+    ab1, h1 = K.gateup_fwd(x, x, offsets, E, w1, w3, I, gather=perm, k=k)
+    assert torch.equal(ab0.view(torch.int16), ab1.view(torch.int16))
+    assert torch.equal(h0.view(torch.int16), h1.view(torch.int16))
+    d_ab = _bf(rows_r + T, 2 * I, scale=0.05, g=g).to(D)
+    outs = []
+    for gathered in (False, True):
+        dw1 = [torch.empty(I, d, dtype=torch.bfloat16, device=D) for _ in range(G)]
+        dw3 = [torch.empty(I, d, dtype=torch.bfloat16, device=D) for _ in range(G)]
+        K.weight_grad(d_ab, None, x if gathered else x_perm, x, offsets, E, rows_r, T, I, dw1, dw3,
+                      torch.bfloat16, b_gather=perm if gathered else None, k=k)
+        outs.append(dw1 + dw3)
+    for a, b in zip(*outs):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    # and one expert's w1 gradient against fp32 arithmetic on the gathered rows
+    e = int(torch.argmax(counts))
+    r0, r1 = int(offsets[e]), int(offsets[e + 1])
+    xs = x.cpu().float()[perm[r0:r1].cpu().long() // k]
+    ref = d_ab[r0:r1, :I].cpu().float().T @ xs
+    assert rel_l2(outs[1][e].cpu(), ref) < 5e-3
+
+
 def _row_products(D, x_r, x_s, do_r, do_s, offsets, E, w1, w3, w2, ab_in, h_in, dab_in, split,
                   short_ws=False):
     """The four row products through the C ABI, with the split workspace or
@@ -443,7 +491,7 @@ def _row_products(D, x_r, x_s, do_r, do_s, offsets, E, w1, w3, w2, ab_in, h_in, 
     st = K._stream()
     ab = torch.empty(rows, 2 * I, dtype=torch.bfloat16, device=D)
     h = torch.empty(rows, I, dtype=torch.bfloat16, device=D)
-    _lib.check(lib.fmoe_gateup_fwd(x_r.data_ptr(), x_s.data_ptr(), offsets.data_ptr(), E, rows_r, rows_s, d, I,
+    _lib.check(lib.fmoe_gateup_fwd(x_r.data_ptr(), None, 0, 0, x_s.data_ptr(), offsets.data_ptr(), E, rows_r, rows_s, d, I,
                                    pa(w1), pa(w3), ab.data_ptr(), h.data_ptr(), wsp, ws_bytes, st), "gateup_fwd")
     o = torch.empty(rows, d, dtype=torch.bfloat16, device=D)
     _lib.check(lib.fmoe_down_fwd(h_in.data_ptr(), offsets.data_ptr(), E, rows_r, rows_s, d, I, pa(w2),
@@ -546,3 +594,26 @@ def test_route_dispatch_matches_two_launches(gpu_device, T, d, E, k, rs):
     assert torch.equal(one[0].cpu(), ridx)
     rc, ro, rp, rpos = mo.dispatch_c(one[0].cpu(), E)
     assert torch.equal(one[4].cpu(), rc) and torch.equal(one[6].cpu(), rp)
+
+
+def test_block_with_gathered_rows_matches_the_default(gpu_device, monkeypatch):
+    # The block's gathered-rows option (moe.GATHER_ROWS: no x_perm; the gate/up
+    # forward and dW1|dW3 read token rows through perm) gives the bits of the
+    # default path, forward and backward.
+    from fusionllm_amd import configs, moe as moe_mod
+    from tests.gpu_util import build_module
+    cfg = configs.C2
+    data = configs.make_block(cfg, seed=3, tokens=2048)
+    outs = []
+    for flag in (False, True):
+        monkeypatch.setattr(moe_mod, "GATHER_ROWS", flag)
+        assert moe_mod.gathers_rows(2048, 2, True) == flag
+        m = build_module(cfg, data, gpu_device)
+        x = data.x.to(gpu_device, torch.bfloat16).requires_grad_(True)
+        y = m(x)
+        y.backward(data.dy.to(gpu_device, torch.bfloat16))
+        outs.append([y.detach(), x.grad] + [p.grad for p in m.parameters()])
+    for a, b in zip(*outs):
+        assert (a is None) == (b is None)
+        if a is not None:
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16))

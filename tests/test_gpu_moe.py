@@ -145,6 +145,18 @@ def test_c3_decode_forward(gpu_device, cfg):
     _compare(cfg, data, g, _oracle_run(cfg, data, g["idx"], backward=False), backward=False)
 
 
+@pytest.mark.parametrize("cfg", configs.C3, ids=lambda c: c.name)
+def test_c3_inference_forward(gpu_device, cfg):
+    # the module's inference branch (no autograd: nothing kept for a backward)
+    data = configs.make_block(cfg, seed=0)
+    m = build_module(cfg, data, gpu_device)
+    with torch.no_grad():
+        y = m(data.x.to(gpu_device, torch.bfloat16))
+    g = {"y": y.cpu(), "idx": m._last_indices.cpu(), "w": m._route_weights.cpu()}
+    _routing_exact(data, g, cfg)
+    _compare(cfg, data, g, _oracle_run(cfg, data, g["idx"], backward=False), backward=False)
+
+
 def test_empty_experts_get_none_grads(gpu_device):
     cfg = configs.BlockConfig("skew-all", 300, dim=256, inter=512, n_experts=8, topk=2)
     data = configs.make_block(cfg, seed=4)

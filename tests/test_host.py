@@ -54,8 +54,10 @@ def test_argument_errors_without_gpu():
     assert lib.fmoe_dispatch_noalloc(None, None, 87382, 2048, 64, 6, None, None, None, None, None, None) == 8
     assert b"1 MiB" in lib.fmoe_status_string(8)
     pp = _lib.ptr_array([0])
-    assert lib.fmoe_gateup_fwd(None, None, None, 1, 10, 0, 96, 128, pp, pp, None, None, None, 0, None) == 2
-    assert lib.fmoe_gateup_fwd(None, None, None, 1, 10, 0, 128, 128, pp, pp, None, None, None, 0, None) == 1
+    assert lib.fmoe_gateup_fwd(None, None, 0, 0, None, None, 1, 10, 0, 96, 128, pp, pp, None, None, None, 0,
+                               None) == 2
+    assert lib.fmoe_gateup_fwd(None, None, 0, 0, None, None, 1, 10, 0, 128, 128, pp, pp, None, None, None, 0,
+                               None) == 1
     assert lib.fmoe_combine_fwd(None, None, None, None, 4, 768, 2, 8, 1, 5, None, None, None) == 4
     # RMSNorm around the block
     assert lib.fmoe_rmsnorm_fwd(None, 0, None, 0, 4, 100, 1e-6, None, None, None) == 2
@@ -70,8 +72,8 @@ def test_argument_errors_without_gpu():
                                    None, 0, None, fake, fake, 100, None) == 6  # workspace too small
     assert lib.fmoe_dx_reduce_norm(None, None, None, None, None, 4, 768, 2, 8, 1, None, None, None, 0,
                                    None, 0, None, None, None, 0, None) == 1  # null inputs
-    assert lib.fmoe_weight_grad(None, None, 8, None, None, 8, None, 1, 10, 0, 128, 128, 0, pp, None, 0,
-                                None, 0, None) == 2
+    assert lib.fmoe_weight_grad(None, None, 8, None, None, 8, None, 0, 0, None, 1, 10, 0, 128, 128, 0, pp, None,
+                                0, None, 0, None) == 2
     # one-launch bf16 casts: count and sizes checked before any pointer is used
     n1 = (ctypes.c_int64 * 1)(-1)
     assert lib.fmoe_cast_bf16(pp, pp, n1, 1, None) == 1
@@ -108,6 +110,38 @@ def test_argument_errors_without_gpu():
                                  None) == 4  # dtype
     assert lib.fmoe_normuon_step(pp1, pp1, pp1, pp1, r1, c1, m1, 1, 0, .02, .9, .95, 1e-8, .1, 1, .1, .05,
                                  None) == 2  # cols not a multiple of 4
+
+
+def test_gathered_rows_argument_checks():
+    from fusionllm_amd import _lib
+    lib = _lib.load()
+    pp = _lib.ptr_array([1 << 20])
+    fake = 1 << 20
+    # decode-sized launches (<= 4096 rows) keep x_perm; gather_k must be positive
+    assert lib.fmoe_gateup_fwd(fake, fake, 2, 100, None, fake, 1, 200, 0, 256, 256, pp, pp, fake, fake, None, 0,
+                               None) == 2
+    assert lib.fmoe_gateup_fwd(fake, fake, 0, 3000, None, fake, 1, 6000, 0, 256, 256, pp, pp, fake, fake, None, 0,
+                               None) == 2
+    assert lib.fmoe_weight_grad(fake, None, 256, fake, None, 256, fake, 0, 100, fake, 1, 10, 0, 256, 256, 256,
+                                pp, None, 0, fake, 1 << 30, None) == 2
+
+
+def test_slot_division_by_multiplication():
+    # The kernels find a routed slot's token as floor(n / k) = high half of
+    # n * m, m = ceil(2^32 / k) (fmoe_common.h: slot_token), exact for
+    # n < 2^29.  Checked at both ends of that range, at every multiple of k
+    # and its neighbours near the top, and on a stride through it.
+    import numpy as np
+    for k in range(1, 9):
+        m = ((1 << 32) + k - 1) // k
+        lo, hi = m & 0xFFFFFFFF, m >> 32
+        top = 1 << 29
+        n = np.concatenate([np.arange(0, 1 << 16), np.arange(top - (1 << 16), top),
+                            np.arange(0, top, 997), (np.arange(top // k - 4096, top // k) * k)[:, None].repeat(3, 1).ravel()
+                            + np.tile([-1, 0, 1], 4096)]).astype(np.uint64)
+        n = n[n < top]
+        got = ((n * np.uint64(lo)) >> np.uint64(32)) + n * np.uint64(hi)
+        assert np.array_equal(got, n // np.uint64(k)), k
 
 
 def test_host_counts_buffer_checks():
