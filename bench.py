@@ -59,6 +59,9 @@ def parse():
                    help="fp32 module and input under bf16 autocast (the trainer's setting); single block")
     p.add_argument("--graph", action="store_true",
                    help="with --fwd-only: time HIP-graph replays of the forward (DecodeGraph)")
+    p.add_argument("--gather-rows", action="store_true",
+                   help="the block reads routed token rows of x through perm (no x_perm copy): "
+                        "fusionllm_amd.moe.GATHER_ROWS")
     p.add_argument("--optimizer", action="store_true",
                    help="time the fused NorMuon step on the block's weight matrices (fp32, as the trainer "
                         "keeps them) instead of the block; its own JSON line")
@@ -442,6 +445,9 @@ def main():
         sys.exit(2)
     from fusionllm_amd import DeepSeekMoE, configs, moe_residual
     from fusionllm_amd import _kernels as K
+    from fusionllm_amd import moe as moe_mod
+    if args.gather_rows:
+        moe_mod.GATHER_ROWS = True
 
     cfg = configs.ALL.get(args.config) or next(
         (c for n, c in configs.ALL.items() if n.split("-")[0] == args.config), None)
@@ -661,6 +667,7 @@ def main():
                    "bias": cfg.bias, "layers": cfg.layers,
                    "pass": "forward" if args.fwd_only else "forward+backward",
                    "launch": "hip-graph replay" if args.graph else "eager",
+                   "routed_rows": "read through perm" if args.gather_rows else "x_perm copy",
                    "params": "fp32 under bf16 autocast" if args.autocast else "bf16"},
         # (null when the step runs no separate GEMM entry point: the fused decode forward)
         "grouped_gemm_mfma_frac": round(gemm_flops / gemm_s / PEAK_BF16_FLOPS, 4) if gemm_s > 0 else None,

@@ -215,10 +215,13 @@ __device__ __forceinline__ uint4 load16(const uint16_t* p, bool nt) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
-template <int MODE>
+// GATHER (GATEUP_FWD only): args.gather is set; a separate instantiation, so
+// that the plain kernel carries none of the gathered path's code.
+template <int MODE, bool GATHER = false>
 __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs args,
                                                                  const int32_t* __restrict__ offsets) {
   using namespace core;
+  constexpr bool GA = MODE == GATEUP_FWD && GATHER;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -274,12 +277,12 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
   const uint16_t* c_b0 = nullptr;  // B operand base(s)
   const uint16_t* c_b1 = nullptr;
   int c_last_row = 0, c_n0 = 0;    // last valid A row of the tile, first B row
-  // GATEUP_FWD: this lane's byte offsets (from c_a) of its A rows of the tile,
-  // rows 64 i + drow clamped to the last valid one.  With args.gather the
-  // routed rows are token rows of x (row r: x row gather[r] / gather_k); the
-  // lane's four indices of an item are loaded when the item before it is set
-  // up (g_pf, vector loads issued after that stage's copies, complete by the
-  // next stage's wait) and consumed one item later.
+  // GA: this lane's byte offsets (from c_a) of its A rows of the tile, rows
+  // 64 i + drow clamped to the last valid one; the routed rows are token rows
+  // of x (row r: x row gather[r] / gather_k).  The lane's four indices of an
+  // item are loaded when the item before it is set up (g_pf, vector loads
+  // issued after that stage's copies, complete by the next stage's wait) and
+  // consumed one item later.
   uint32_t a_off[LA];
   int32_t g_pf[LA] = {0, 0, 0, 0};
   bool g_pf_routed = false;  // the prefetched item is a routed tile (its rows are gathered)
@@ -309,7 +312,7 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
     split_item(sp, nk, b + ti * NP, tile, c_k0, c_kn, slot);
     int g, tm, tn, row_base, M;
     locate_tile(args, offsets, tiles_n, tile, g, tm, tn, row_base, M);
-    const bool gathered = MODE == GATEUP_FWD && args.gather != nullptr && g < args.E;
+    const bool gathered = GA && g < args.E;
     const uint16_t* A = gathered ? args.a_routed
                         : (g < args.E || args.a_shared == nullptr) ? args.a_routed + static_cast<int64_t>(row_base) * args.lda
                                                                    : args.a_shared;
@@ -318,7 +321,7 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
     c_b0 = args.b0[g];
     c_b1 = args.b1[g];
     c_n0 = tn * TN_COLS;
-    if constexpr (MODE == GATEUP_FWD) {
+    if constexpr (GA) {
       if (gathered) {
         // g_pf holds this item's indices (loaded one item ahead, a stage wait
         // has normally passed since; the wait here covers every operation older
@@ -337,15 +340,13 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
         for (int i = 0; i < LA; ++i)
           a_off[i] = static_cast<uint32_t>(min(64 * i + drow, c_last_row) * static_cast<int>(args.lda) + dchunk * 8) * 2u;
       }
-      if (args.gather != nullptr) prefetch_rows(ti + 1);
+      prefetch_rows(ti + 1);
     }
   };
-  if constexpr (MODE == GATEUP_FWD) {
-    if (args.gather != nullptr) {
-      // the first item's indices, waited for at once
-      prefetch_rows(0);
-      asm volatile("s_waitcnt vmcnt(0)" : "+v"(g_pf[0]), "+v"(g_pf[1]), "+v"(g_pf[2]), "+v"(g_pf[3])::"memory");
-    }
+  if constexpr (GA) {
+    // the first item's indices, waited for at once
+    prefetch_rows(0);
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(g_pf[0]), "+v"(g_pf[1]), "+v"(g_pf[2]), "+v"(g_pf[3])::"memory");
   }
   copy_tile(0);
   const int lda = static_cast<int>(args.lda), ldb = static_cast<int>(args.ldb);
@@ -354,7 +355,7 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
     const int kofs = (c_k0 + c_kt) * BK;
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
-      if constexpr (MODE == GATEUP_FWD) {
+      if constexpr (GA) {
         copy16(st + i * 8192, c_a + kofs, a_off[i]);
       } else {
         const int r = min(64 * i + drow, c_last_row);
@@ -1045,6 +1046,9 @@ __device__ __forceinline__ bf16x8 tr_frag(uint32_t addr) {
   return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// GATHER: args.b_gather is set (a separate instantiation, so that the plain
+// kernel carries none of the gathered path's code).
+template <bool GATHER>
 __global__ __launch_bounds__(core::NT, 1) void wgrad_tr_kernel(const WgradArgs args,
                                                                const int32_t* __restrict__ offsets) {
   using namespace core;
@@ -1105,7 +1109,7 @@ __global__ __launch_bounds__(core::NT, 1) void wgrad_tr_kernel(const WgradArgs a
   const int nk = (k_end - k_begin + BK - 1) / BK;
   const bool shared_sep = (g >= args.E);
   const uint16_t* A = (shared_sep && args.a_shared) ? args.a_shared : args.a_routed + static_cast<int64_t>(row_base) * args.lda;
-  const bool gathered = args.b_gather != nullptr && !shared_sep;
+  const bool gathered = GATHER && !shared_sep;
   const uint16_t* B = (shared_sep && args.b_shared) ? args.b_shared
                       : gathered ? args.b_routed
                                  : args.b_routed + static_cast<int64_t>(row_base) * args.ldb;
@@ -1385,7 +1389,12 @@ int launch_rows(GemmArgs& a, int64_t rows_routed, int64_t rows_shared, int E, vo
     // count from below, so such a run skips the header and the reduction.
     const int64_t tiles_lo = (ceil_div(rows_routed, core::BM) + ceil_div(rows_shared, core::BM)) * tiles_n;
     if (a.small_max == 0 && tiles_lo / grid >= kSplitMaxRounds) a.split_ws = nullptr;
-    rows_gemm_kernel<MODE><<<dim3(grid), dim3(core::NT), 0, as_stream(stream)>>>(a, a.offsets);
+    bool gathered = false;
+    if constexpr (MODE == GATEUP_FWD) {
+      gathered = a.gather != nullptr;
+      if (gathered) rows_gemm_kernel<MODE, true><<<dim3(grid), dim3(core::NT), 0, as_stream(stream)>>>(a, a.offsets);
+    }
+    if (!gathered) rows_gemm_kernel<MODE, false><<<dim3(grid), dim3(core::NT), 0, as_stream(stream)>>>(a, a.offsets);
     if (a.split_ws != nullptr) {
       if constexpr (MODE == DOWN_FWD || MODE == GATEUP_BWD)
         split_reduce_kernel<<<dim3(grid * kReduceParts), dim3(256), 0, as_stream(stream)>>>(
@@ -1657,7 +1666,10 @@ extern "C" int fmoe_weight_grad(const void* a_routed, const void* a_shared, int6
   const int64_t tiles = ceil_div(m_out, core::BM) * ceil_div(n_out, core::BN);
   const int64_t max_chunks = (rows_routed + rows_shared) / a.kc + G;
   hipStream_t s = as_stream(stream);
-  wgrad_tr_kernel<<<dim3(max_chunks * tiles), dim3(core::NT), 0, s>>>(a, offsets);
+  if (b_gather)
+    wgrad_tr_kernel<true><<<dim3(max_chunks * tiles), dim3(core::NT), 0, s>>>(a, offsets);
+  else
+    wgrad_tr_kernel<false><<<dim3(max_chunks * tiles), dim3(core::NT), 0, s>>>(a, offsets);
   const int64_t mn = m_out * n_out;
   wgrad_reduce_kernel<<<dim3(ceil_div(mn, 256 * 8), G), dim3(256), 0, s>>>(a);
   return launch_status();

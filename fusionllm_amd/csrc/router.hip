@@ -242,6 +242,165 @@ __global__ __launch_bounds__(kRouterTok / R * kRouterLanes) void router_fwd_kern
   }
 }
 
+// Many experts (E > 16, e.g. 64 at dim 2048): router_fwd_kernel reads every
+// gate value from LDS once per token (32 bytes of fp32 per 8 FMAs), and its
+// LDS reads bound it (C5: 426 us).  Here each 16-lane group sums a 4-token x
+// S-expert block of logits (S = EB / 8): for every chunk it reads the 4
+// tokens' x chunks and the S experts' gate chunks from LDS once and does
+// 4 x S x 8 FMAs with them (1.5 bytes of LDS per FMA at S = 8).  The 32
+// tokens of the workgroup (the router's blocks, as the dispatch histogram
+// expects) are 8 token blocks, the experts 8 expert blocks: 64 groups, 1024
+// threads, so that a lane holds 4 S sums and four waves share each SIMD.
+// dim is walked in slices of 128 elements (one 8-element chunk per lane),
+// staged in LDS as fp32 (x and gate, each chunk as two float4 planes),
+// double buffered, the next slice's loads in flight while the current one is
+// summed.  Each (token, expert) sum keeps the order at the top of this file:
+// lane j takes chunks j, j + 16, ... in ascending order, elements in order,
+// fmaf from 0, then the butterfly; so it gives the bits of
+// router_fwd_kernel.  Scores and top-k as there.
+constexpr int kWideTB = 4;         // tokens per group block
+constexpr int kWideThreads = 1024;
+
+template <int EB>
+__global__ __launch_bounds__(kWideThreads) void router_wide_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg,
+    const uint16_t* __restrict__ bg, int T, int dim, int E, int k, float route_scale,
+    int32_t* __restrict__ idx, int64_t* __restrict__ idx64, float* __restrict__ wout,
+    float* __restrict__ vout, int32_t* __restrict__ block_hist) {
+  constexpr int S = EB / 8;  // experts per group block
+  constexpr int NT = kWideThreads;
+  constexpr int NTB = kRouterTok / kWideTB;  // token blocks
+  static_assert(NTB * 8 * kRouterLanes == NT, "8 token blocks x 8 expert blocks of 16 lanes");
+  // slice planes: [buffer][row][lane] of float4 (elements 0-3 / 4-7 of the row's chunk)
+  __shared__ float4 xlo[2][kRouterTok][kRouterLanes], xhi[2][kRouterTok][kRouterLanes];
+  __shared__ float4 glo[2][EB][kRouterLanes], ghi[2][EB][kRouterLanes];
+  __shared__ float lsh[kRouterTok * EB];
+  __shared__ float bsh[EB];
+  __shared__ int hcnt[EB];
+  const int tid = threadIdx.x;
+  const int lane16 = tid % kRouterLanes, grp = tid / kRouterLanes;
+  const int tb = grp % NTB, eb = grp / NTB;  // token block, expert block
+  const int nchunk = dim / 8, nslice = (nchunk + kRouterLanes - 1) / kRouterLanes;
+  if (block_hist != nullptr && tid < EB) hcnt[tid] = 0;  // ordered by the first barrier below
+  if (tid < E) bsh[tid] = bf2f(bg[tid]);
+  const int t0 = blockIdx.x * kRouterTok;
+
+  // staging of slice q: x rows (32 tokens x 16 chunks: threads 0 .. 511, one
+  // chunk each) and gate rows (EB x 16 chunks: one chunk per thread up to EB * 16)
+  constexpr int XCH = kRouterTok * kRouterLanes, GCH = EB * kRouterLanes;
+  static_assert(XCH <= NT && GCH <= NT, "one chunk per thread");
+  // two register sets of staged chunks (slices two apart), so that two
+  // slices' loads are in flight while one is summed
+  uint4 xv[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+  uint4 gv[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+  const int s_row = tid / kRouterLanes, s_ch = tid % kRouterLanes;
+  const uint16_t* xrow = x + static_cast<int64_t>(min(t0 + min(s_row, kRouterTok - 1), T - 1)) * dim;
+  const uint16_t* grow = wg + static_cast<int64_t>(min(s_row, E - 1)) * dim;
+  auto load_slice = [&](int q, uint4& xr, uint4& gr) {
+    const int c = q * kRouterLanes + s_ch;
+    if (tid < XCH) xr = c < nchunk ? reinterpret_cast<const uint4*>(xrow)[c] : make_uint4(0, 0, 0, 0);
+    if (tid < GCH)
+      gr = (s_row < E && c < nchunk) ? reinterpret_cast<const uint4*>(grow)[c] : make_uint4(0, 0, 0, 0);
+  };
+  auto store_slice = [&](int buf, const uint4& xr, const uint4& gr) {
+    float f[8];
+    if (tid < XCH) {
+      unpack8(xr, f);
+      xlo[buf][s_row][s_ch] = make_float4(f[0], f[1], f[2], f[3]);
+      xhi[buf][s_row][s_ch] = make_float4(f[4], f[5], f[6], f[7]);
+    }
+    if (tid < GCH) {
+      unpack8(gr, f);
+      glo[buf][s_row][s_ch] = make_float4(f[0], f[1], f[2], f[3]);
+      ghi[buf][s_row][s_ch] = make_float4(f[4], f[5], f[6], f[7]);
+    }
+  };
+
+  float acc[kWideTB][S];
+#pragma unroll
+  for (int t = 0; t < kWideTB; ++t)
+#pragma unroll
+    for (int e = 0; e < S; ++e) acc[t][e] = 0.0f;
+  auto sum_slice = [&](int q) {
+    const int buf = q & 1;
+    if (q * kRouterLanes + lane16 < nchunk) {
+      float xf[kWideTB][8];
+#pragma unroll
+      for (int t = 0; t < kWideTB; ++t) {
+        const float4 a = xlo[buf][tb * kWideTB + t][lane16], b = xhi[buf][tb * kWideTB + t][lane16];
+        xf[t][0] = a.x; xf[t][1] = a.y; xf[t][2] = a.z; xf[t][3] = a.w;
+        xf[t][4] = b.x; xf[t][5] = b.y; xf[t][6] = b.z; xf[t][7] = b.w;
+      }
+#pragma unroll
+      for (int e = 0; e < S; ++e) {
+        const float4 a = glo[buf][eb * S + e][lane16], b = ghi[buf][eb * S + e][lane16];
+        const float wf[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int t = 0; t < kWideTB; ++t)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[t][e] = fmaf(xf[t][i], wf[i], acc[t][e]);
+      }
+    }
+  };
+  // slice q: summed from LDS buffer q % 2; its chunks were loaded into
+  // register set q % 2 two slices earlier.  After summing slice q: slice
+  // q + 1 goes from its register set to the other buffer (last read while
+  // summing q - 1, before the barrier that ended it), and that set loads
+  // slice q + 3.
+  load_slice(0, xv[0], gv[0]);
+  if (nslice > 1) load_slice(1, xv[1], gv[1]);
+  store_slice(0, xv[0], gv[0]);
+  if (nslice > 2) load_slice(2, xv[0], gv[0]);
+  __syncthreads();
+  for (int q = 0; q < nslice; q += 2) {
+    sum_slice(q);
+    if (q + 1 < nslice) {
+      store_slice(1, xv[1], gv[1]);
+      if (q + 3 < nslice) load_slice(q + 3, xv[1], gv[1]);
+      __syncthreads();
+      sum_slice(q + 1);
+      if (q + 2 < nslice) {
+        store_slice(0, xv[0], gv[0]);
+        if (q + 4 < nslice) load_slice(q + 4, xv[0], gv[0]);
+        __syncthreads();
+      }
+    }
+  }
+#pragma unroll
+  for (int off = kRouterLanes / 2; off >= 1; off >>= 1)
+#pragma unroll
+    for (int t = 0; t < kWideTB; ++t)
+#pragma unroll
+      for (int e = 0; e < S; ++e) acc[t][e] = acc[t][e] + xor_lane(acc[t][e], off);
+  // every lane of the group holds the block's logits; lane j writes those of
+  // its (t, e) with (t * S + e) % 16 == j
+#pragma unroll
+  for (int t = 0; t < kWideTB; ++t)
+#pragma unroll
+    for (int e = 0; e < S; ++e)
+      if ((t * S + e) % kRouterLanes == lane16 && eb * S + e < E) lsh[(tb * kWideTB + t) * EB + eb * S + e] = acc[t][e];
+  __syncthreads();
+
+  // scores and top-k: group g < 32 takes token g of the workgroup (as router_fwd_kernel)
+  if (grp < kRouterTok) {
+    float* lg = lsh + grp * EB;
+    for (int e = lane16; e < E; e += kRouterLanes) lg[e] = fm_sigmoid(lg[e] + bsh[e]);
+  }
+  __syncthreads();
+  if (grp < kRouterTok) {
+    const int t = t0 + grp;
+    float sc[EB];
+#pragma unroll
+    for (int e = 0; e < EB; ++e) sc[e] = (e < E) ? lsh[grp * EB + e] : 0.0f;
+    pick_topk<EB>(sc, E, k, route_scale, lane16, t < T, t, idx, idx64, wout, vout, nullptr,
+                  block_hist != nullptr ? hcnt : nullptr);
+  }
+  if (block_hist != nullptr) {
+    __syncthreads();
+    if (tid < E) block_hist[static_cast<int64_t>(blockIdx.x) * E + tid] = hcnt[tid];
+  }
+}
+
 // Decode-sized batches (T <= kRouterSmallT): one workgroup per token and one
 // 16-lane group per expert (group g takes experts g, g + G, ...), so that the
 // logits of a token are formed side by side instead of one expert after
@@ -619,6 +778,10 @@ extern "C" int fmoe_router_fwd(const void* x, const void* gate_w, const void* ga
       router_small_kernel<EB, NQ><<<dim3(blocks), dim3(threads), 0, s>>>(xs, ws, bs, (int)dim,         \
                                                                          n_experts, k, route_scale,  \
                                                                          idx, idx64, weights, topv); \
+    else if (EB >= 32)                                                                                \
+      router_wide_kernel<(EB >= 32 ? EB : 32)><<<dim3(blocks), dim3(kWideThreads), 0, s>>>(xs, ws, bs, (int)T, \
+                                                                    (int)dim, n_experts, k, route_scale, \
+                                                                    idx, idx64, weights, topv, nullptr); \
     else                                                                                              \
       router_fwd_kernel<EB, NQ, kRouterPerGroup><<<dim3(blocks), dim3(threads), 0, s>>>(xs, ws, bs, (int)T, (int)dim,  \
                                                                        n_experts, k, route_scale,    \
@@ -652,9 +815,16 @@ int launch_router_hist(const uint16_t* xs, const uint16_t* ws, const uint16_t* b
   const int threads = kRouterThreads;
   const int64_t blocks = ceil_div(T, kRouterTok);
 #define FMOE_ROUTER_H(EB, NQ)                                                                          \
-  router_fwd_kernel<EB, NQ, kRouterPerGroup><<<dim3(blocks), dim3(threads), 0, s>>>(xs, ws, bs, (int)T, (int)dim, n_experts, \
+  do {                                                                                                 \
+    if (EB >= 32)                                                                                      \
+      router_wide_kernel<(EB >= 32 ? EB : 32)><<<dim3(blocks), dim3(kWideThreads), 0, s>>>(xs, ws, bs, (int)T, \
+                                                                    (int)dim, n_experts, k, route_scale, \
+                                                                    idx, idx64, weights, topv, block_hist); \
+    else                                                                                               \
+      router_fwd_kernel<EB, NQ, kRouterPerGroup><<<dim3(blocks), dim3(threads), 0, s>>>(xs, ws, bs, (int)T, (int)dim, n_experts, \
                                                                    k, route_scale, idx, idx64, weights,   \
-                                                                   topv, block_hist)
+                                                                   topv, block_hist);                     \
+  } while (0)
 #define FMOE_ROUTER_H_E(NQ)                              \
   do {                                                   \
     if (n_experts <= 8) FMOE_ROUTER_H(8, NQ);            \

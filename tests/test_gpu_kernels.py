@@ -40,7 +40,12 @@ def _check_router(x, gw, gb, k, rs, dev):
                                         (512, 2048, 64, 6, 1.0), (200, 256, 16, 4, 1.0), (64, 64, 3, 3, 1.0),
                                         # decode-sized batches (one workgroup per token) and the boundary
                                         (128, 2048, 64, 6, 1.0), (129, 768, 8, 2, 1.0), (5, 768, 8, 2, 2.5),
-                                        (17, 256, 33, 8, 1.0)])
+                                        (17, 256, 33, 8, 1.0),
+                                        # more than 16 experts above 128 tokens (8-token x S-expert
+                                        # blocks per 16-lane group): dim not a multiple of 128, E not a
+                                        # multiple of 8, a partial last workgroup
+                                        (300, 192, 40, 5, 1.0), (257, 64, 64, 8, 1.0), (1000, 1344, 48, 6, 2.5),
+                                        (4097, 2048, 64, 6, 1.0), (200, 768, 17, 3, 1.0)])
 def test_router_bit_exact(gpu_device, T, d, E, k, rs):
     x, gw, gb = _routing_inputs(T, d, E, seed=T + E)
     _check_router(x, gw, gb, k, rs, gpu_device)
