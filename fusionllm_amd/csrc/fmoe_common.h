@@ -48,8 +48,13 @@ __device__ __forceinline__ void unpack8(const uint4& v, float* f) {
   f[4] = __uint_as_float(v.z << 16); f[5] = __uint_as_float(v.z & 0xffff0000u);
   f[6] = __uint_as_float(v.w << 16); f[7] = __uint_as_float(v.w & 0xffff0000u);
 }
+// Two floats to a bf16 pair with one v_cvt_pk_bf16_f32 (round to nearest
+// even, as f2bf; two scalar conversions and the shift and or to join them
+// took four instructions).
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 __device__ __forceinline__ uint4 pack8(const float* f) {
   uint4 v;

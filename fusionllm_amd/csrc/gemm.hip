@@ -215,6 +215,100 @@ __device__ __forceinline__ uint4 load16(const uint16_t* p, bool nt) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
+// SwiGLU backward of 8 columns (h = s * b, s = bf16(silu(a)); dh arrives
+// bf16-rounded): da = bf16(bf16(dh * b) * silu'(a)), db = bf16(dh * s), with
+// silu(a) = a * sg and silu'(a) = sg * (1 + a (1 - sg)) = sg + silu(a) (1 - sg).
+__device__ __forceinline__ void swiglu_bwd8(const uint4& dhv, const uint4& av, const uint4& bv, uint4& dav,
+                                            uint4& dbv) {
+  float dh[8], af[8], bfv[8], da[8], db[8];
+  unpack8(dhv, dh);
+  unpack8(av, af);
+  unpack8(bv, bfv);
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const float sg0 = fast_sigmoid(af[e]), sg1 = fast_sigmoid(af[e + 1]);
+    const float sa0 = af[e] * sg0, sa1 = af[e + 1] * sg1;
+    float sv0 = sa0, sv1 = sa1, ds0 = dh[e] * bfv[e], ds1 = dh[e + 1] * bfv[e + 1];
+    bf_round2(sv0, sv1);
+    bf_round2(ds0, ds1);
+    da[e] = ds0 * fmaf(sa0, 1.0f - sg0, sg0);
+    da[e + 1] = ds1 * fmaf(sa1, 1.0f - sg1, sg1);
+    db[e] = dh[e] * sv0;
+    db[e + 1] = dh[e + 1] * sv1;
+  }
+  dav = pack8(da);
+  dbv = pack8(db);
+}
+
+// Down-backward epilogue of a full tile (this wave's 64 x 128 block of dh in
+// acc).  The SwiGLU backward costs about as many instructions per element as
+// the block has accumulators, so the block is first staged whole: dh rounded
+// to bf16, through the wave's 4 KB of LDS one 16-row slice at a time, read
+// back as 16-byte row segments (64 registers, the accumulators are then
+// free).  The a|b loads then run as a pipeline two slices deep (the loads of
+// slice i + 2 issued while slice i is computed and stored); a deeper one
+// measured no faster.  Row pointers are uniform (scalar registers); a lane
+// adds one offset.  Measured at C2 against the previous slice-by-slice
+// epilogue (a|b of one slice in flight while it was staged): 266-279 ->
+// 258-265 us, bit-identical.
+__device__ __forceinline__ void down_bwd_full_epilogue(const GemmArgs& args, const f32x4 (&acc)[core::FM][core::FN],
+                                                       uint8_t* ep, int el, int64_t grow0, int col0) {
+  using namespace core;
+  uint4 dhv[FM][4];
+  {
+    const int r = el & 15;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        // chunk c of row r at slot c ^ r (256-byte rows)
+        const int col = j * 16 + (el >> 4) * 4;
+        const uint32_t off = r * 256 + ((((col >> 3) ^ r)) << 4) + (col & 7) * 2;
+        *reinterpret_cast<uint2*>(ep + off) =
+            make_uint2(pack2(acc[i][j][0], acc[i][j][1]), pack2(acc[i][j][2], acc[i][j][3]));
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int rr = t * 4 + (el >> 4), c = el & 15;
+        dhv[i][t] = *reinterpret_cast<const uint4*>(ep + rr * 256 + ((c ^ rr) << 4));
+      }
+    }
+  }
+  // lane: rows 4 t + el / 16 of each slice, columns col0 + 8 (el % 16) .. +7
+  const uint8_t* abase = reinterpret_cast<const uint8_t*>(args.aux + grow0 * args.ldaux + col0);
+  const uint32_t aoff = static_cast<uint32_t>((el >> 4) * static_cast<int>(args.ldaux) + (el & 15) * 8) * 2u;
+  const int64_t astep = args.ldaux * 2 * 4;  // bytes per 4 rows
+  uint8_t* cbase = reinterpret_cast<uint8_t*>(args.c0 + grow0 * args.ldc0 + col0);
+  const uint32_t coff = static_cast<uint32_t>((el >> 4) * static_cast<int>(args.ldc0) + (el & 15) * 8) * 2u;
+  const int64_t cstep = args.ldc0 * 2 * 4;
+  const int64_t binter = args.inter * 2;  // bytes from a to b (and from da to db)
+  constexpr int kDepth = 2;               // slices of a|b loads in flight
+  uint4 pa[FM][4], pb[FM][4];
+  auto load_slice = [&](int i) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint8_t* rp = abase + (i * 4 + t) * astep;
+      pa[i][t] = load16(reinterpret_cast<const uint16_t*>(rp + aoff), true);
+      pb[i][t] = load16(reinterpret_cast<const uint16_t*>(rp + binter + aoff), true);
+    }
+  };
+  asm volatile("" ::: "memory");  // the loads are not hoisted into the staging above
+#pragma unroll
+  for (int i = 0; i < kDepth; ++i) load_slice(i);
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    if (i > 0 && i + kDepth - 1 < FM) load_slice(i + kDepth - 1);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      uint4 dav, dbv;
+      swiglu_bwd8(dhv[i][t], pa[i][t], pb[i][t], dav, dbv);
+      uint8_t* rp = cbase + (i * 4 + t) * cstep;
+      store16(reinterpret_cast<uint16_t*>(rp + coff), dav, true);
+      store16(reinterpret_cast<uint16_t*>(rp + binter + coff), dbv, true);
+    }
+  }
+}
+
 // GATHER (GATEUP_FWD only): args.gather is set; a separate instantiation, so
 // that the plain kernel carries none of the gathered path's code.
 template <int MODE, bool GATHER = false>
@@ -474,11 +568,20 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
       const int col0 = tn * TN_COLS + wn * (TN_COLS / WN);  // first output column of this wave
       const bool full = rows_valid == BM && (tn + 1) * TN_COLS <= args.N;
       const int64_t grow0 = static_cast<int64_t>(row_base) + tm * BM + wm * WTM;
+      bool epi_done = false;
+      if constexpr (MODE == DOWN_BWD) {
+        if (full) {
+          down_bwd_full_epilogue(args, acc, ep, el, grow0, col0);
+          epi_done = true;
+        }
+      }
+      if (!epi_done)
   #pragma unroll
       for (int i = 0; i < FM; ++i) {
-        // DOWN_BWD: a|b of the 16 rows go in flight before the staging below,
-        // all 8 loads at once (rows and columns clamped into the tile, so the
-        // addresses stay valid for a partial tile; such values are not stored)
+        // DOWN_BWD (partial tiles; full ones took down_bwd_full_epilogue): a|b
+        // of the 16 rows go in flight before the staging below, all 8 loads at
+        // once (rows and columns clamped into the tile, so the addresses stay
+        // valid for a partial tile; such values are not stored)
         uint4 pa[4], pb[4];
         if constexpr (MODE == DOWN_BWD) {
   #pragma unroll
@@ -522,26 +625,10 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
             // da = bf16(bf16(dh * b) * silu'(a)), db = bf16(dh * s)
             const int hc = col0 + c * 8;
             if (full || (lrow < rows_valid && hc < args.N)) {
-              float dh[8], af[8], bfv[8], da[8], db[8];
-              unpack8(v, dh);
-              unpack8(pa[t], af);
-              unpack8(pb[t], bfv);
-  #pragma unroll
-              for (int e = 0; e < 8; e += 2) {
-                // silu(a) = a * sg (sv: rounded); silu'(a) = sg * (1 + a (1 - sg))
-                // = sg + silu(a) * (1 - sg)
-                const float sg0 = fast_sigmoid(af[e]), sg1 = fast_sigmoid(af[e + 1]);
-                const float sa0 = af[e] * sg0, sa1 = af[e + 1] * sg1;
-                float sv0 = sa0, sv1 = sa1, ds0 = dh[e] * bfv[e], ds1 = dh[e + 1] * bfv[e + 1];
-                bf_round2(sv0, sv1);
-                bf_round2(ds0, ds1);
-                da[e] = ds0 * fmaf(sa0, 1.0f - sg0, sg0);
-                da[e + 1] = ds1 * fmaf(sa1, 1.0f - sg1, sg1);
-                db[e] = dh[e] * sv0;
-                db[e + 1] = dh[e + 1] * sv1;
-              }
-              store16(args.c0 + grow * args.ldc0 + hc, pack8(da), true);
-              store16(args.c0 + grow * args.ldc0 + args.inter + hc, pack8(db), true);
+              uint4 dav, dbv;
+              swiglu_bwd8(v, pa[t], pb[t], dav, dbv);
+              store16(args.c0 + grow * args.ldc0 + hc, dav, true);
+              store16(args.c0 + grow * args.ldc0 + args.inter + hc, dbv, true);
             }
           } else {
             const int oc = col0 + c * 8;
@@ -594,6 +681,20 @@ __global__ __launch_bounds__(core::NT, 1) void rows_gemm_kernel(const GemmArgs a
       for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     asm volatile("s_nop 1" ::: "memory");  // VALU writes -> MFMA reads of the accumulators
     last_epi = it;
+    if constexpr (MODE == DOWN_BWD) {
+      // The fragments the last K step read for the next tile are read again
+      // (its first stage has landed, waited for above; after the last tile
+      // the reads harmlessly re-read a stage), so that their registers are
+      // free during the epilogue, which needs them for the a|b loads (no
+      // branch in the K loop: a K step that skipped the reads before an
+      // epilogue kept both sets live and spilled).
+      const uint32_t nst = sbase + ((it + 1) & 1) * STAGE;
+      typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
+#pragma unroll
+      for (int p = 0; p < FN; ++p) P[p] = trb_frag(nst + (xb ^ (static_cast<uint32_t>(p) << 5)));
+#pragma unroll
+      for (int q = 0; q < 4; ++q) Q[0][q] = *(const lds_bf16x8*)(uintptr_t)(nst + xa + 2048u * q);
+    }
     if (++e_ti < my_items) {
       int k0_;
       split_item(sp, nk, b + e_ti * NP, e_tile, k0_, e_kn, e_slot);
@@ -730,24 +831,10 @@ __global__ __launch_bounds__(256) void split_reduce_down_bwd_kernel(const GemmAr
     if (row >= t.d.y || c >= t.d.w) continue;
     const int64_t grow = static_cast<int64_t>(t.d.x) + row;
     const int hc = t.d.z + c;
-    float dh[8], af[8], bfv[8], da[8], db[8];
-    unpack8(pack8(acc[q]), dh);  // dh arrives bf16-rounded, as in the tile epilogue
-    unpack8(la[q], af);
-    unpack8(lb[q], bfv);
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      const float sg0 = fast_sigmoid(af[e]), sg1 = fast_sigmoid(af[e + 1]);
-      const float sa0 = af[e] * sg0, sa1 = af[e + 1] * sg1;
-      float sv0 = sa0, sv1 = sa1, ds0 = dh[e] * bfv[e], ds1 = dh[e + 1] * bfv[e + 1];
-      bf_round2(sv0, sv1);
-      bf_round2(ds0, ds1);
-      da[e] = ds0 * fmaf(sa0, 1.0f - sg0, sg0);
-      da[e + 1] = ds1 * fmaf(sa1, 1.0f - sg1, sg1);
-      db[e] = dh[e] * sv0;
-      db[e + 1] = dh[e + 1] * sv1;
-    }
-    store16(args.c0 + grow * args.ldc0 + hc, pack8(da), true);
-    store16(args.c0 + grow * args.ldc0 + args.inter + hc, pack8(db), true);
+    uint4 dav, dbv;
+    swiglu_bwd8(pack8(acc[q]), la[q], lb[q], dav, dbv);  // dh arrives bf16-rounded, as in the tile epilogue
+    store16(args.c0 + grow * args.ldc0 + hc, dav, true);
+    store16(args.c0 + grow * args.ldc0 + args.inter + hc, dbv, true);
   }
 }
 
