@@ -62,15 +62,6 @@ constexpr int kScanThreads = 1024;
 constexpr int kScanWaves = kScanThreads / 64;
 constexpr int kScanBatch = 16;  // loads per lane in flight on the wave-row path
 
-__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int u = __shfl_up(v, off, 64);
-    if (lane >= off) v += u;
-  }
-  return v;
-}
-
 // The expert counts also go to counts_host (nullable): host memory that the
 // caller reads once the stream has passed this kernel, written with
 // system-scope stores (through to memory, visible to the host).
@@ -158,10 +149,12 @@ __global__ __launch_bounds__(kScanThreads) void dispatch_scan_kernel(
     if (lane == 0) total[e] = sum;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int q = 0; q < E; ++q) { start[q] = run; run += total[q]; }
-    start[E] = run;
+  if (threadIdx.x < 64) {
+    const int lane0 = threadIdx.x;
+    const int t = lane0 < E ? total[lane0] : 0;
+    const int incl = wave_incl_scan(t, lane0);
+    if (lane0 < E) start[lane0] = incl - t;
+    if (lane0 == 63) start[E] = incl;
   }
   __syncthreads();
   for (int e = threadIdx.x; e < E; e += kScanThreads) {
@@ -350,14 +343,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_small_kernel(
     pending &= ~m;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int q = 0; q < E; ++q) {
-      start[q] = run;
-      for (int w = 0; w < kDispWaves; ++w) run += wcount[w][q];
-    }
-    start[E] = run;
-  }
+  scan_wave_counts<kDispWaves>(wcount, E, start);
   __syncthreads();
   if (valid) {
     int pos = start[e] + rank;

@@ -63,6 +63,36 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
   return v;
 }
 
+// ---- wave scans -------------------------------------------------------------
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int u = __shfl_up(v, off, 64);
+    if (lane >= off) v += u;
+  }
+  return v;
+}
+
+// Expert offsets of a counting sort from per-wave counts (E <= 64):
+// start[q] = sum over experts q' < q of sum_w wcount[w][q'], start[E] = the
+// total.  Wave 0 does it: lane q adds its expert's W wave counts (independent
+// LDS reads), then one exclusive scan over the lanes (a single thread walking
+// E x W counts waited for each LDS read in turn: about 3 us at E = 8, W = 8).
+template <int W>
+__device__ __forceinline__ void scan_wave_counts(const int (*wcount)[FMOE_MAX_EXPERTS], int E, int* start) {
+  if (threadIdx.x < 64) {
+    const int q = threadIdx.x;
+    int t = 0;
+    if (q < E)
+#pragma unroll
+      for (int w = 0; w < W; ++w) t += wcount[w][q];
+    const int incl = wave_incl_scan(t, q);
+    if (q < E) start[q] = incl - t;
+    if (q == 63) start[E] = incl;
+  }
+}
+
 // ---- exp and sigmoid for the router ----------------------------------------
 // e^x by Cody-Waite range reduction x = n*ln2 + r (|r| <= ln2/2) and the
 // degree-7 Taylor polynomial of e^r (truncation error < 6e-9 relative), then

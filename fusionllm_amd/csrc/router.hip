@@ -416,9 +416,12 @@ __global__ __launch_bounds__(512) void router_small_kernel(
     int32_t* __restrict__ idx, int64_t* __restrict__ idx64, float* __restrict__ wout,
     float* __restrict__ vout) {
   __shared__ float lsh[EB];
+  __shared__ float bsh[EB];
   const int lane16 = threadIdx.x % kRouterLanes;
   const int grp = threadIdx.x / kRouterLanes, ngrp = blockDim.x / kRouterLanes;
   const int t = blockIdx.x;
+  // the bias, loaded beside the logits' operands rather than after them
+  if (threadIdx.x < E) bsh[threadIdx.x] = bf2f(bg[threadIdx.x]);
   const int nchunk = dim / 8;
   const uint4* xrow = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t) * dim);
   uint4 xr[NQ];
@@ -451,7 +454,9 @@ __global__ __launch_bounds__(512) void router_small_kernel(
     if (lane16 == 0) lsh[e] = acc;
   }
   __syncthreads();
-  if (grp == 0) route_token<EB>(lsh, bg, E, k, route_scale, lane16, true, t, idx, idx64, wout, vout);
+  if (grp == 0)
+    route_token<EB>(lsh, static_cast<const float*>(bsh), E, k, route_scale, lane16, true, t, idx, idx64, wout,
+                    vout);
 }
 
 // ---- routing and dispatch of a tiny batch in one launch ---------------------
@@ -481,10 +486,13 @@ __global__ __launch_bounds__(kTinyThreads) void route_dispatch_tiny_kernel(
   __shared__ int wcount[kTinyWaves][FMOE_MAX_EXPERTS];
   __shared__ int start[FMOE_MAX_EXPERTS + 1];
   __shared__ uint4 x_sh[kTinyT * (kRouterMaxDim / 8)];  // the token rows, for the gather
+  __shared__ float bsh[FMOE_MAX_EXPERTS];
   const int tid = threadIdx.x, lane16 = tid % kRouterLanes, grp = tid / kRouterLanes;
   const int lane = tid & 63, wave = tid >> 6;
   const int nchunk = dim / 8, n_slots = T * k;
   for (int i = tid; i < kTinyWaves * E; i += kTinyThreads) wcount[i / E][i % E] = 0;
+  // the bias, loaded beside the logits' operands rather than after them
+  if (tid < E) bsh[tid] = bf2f(bg[tid]);
 
   // 1. logits
   for (int p = grp; p < T * E; p += kTinyThreads / kRouterLanes) {
@@ -524,7 +532,8 @@ __global__ __launch_bounds__(kTinyThreads) void route_dispatch_tiny_kernel(
 
   // 2. routing: group t routes token t
   if (grp < T)
-    route_token<EB>(lsh + grp * EB, bg, E, k, route_scale, lane16, true, grp, idx, idx64, wout, vout, idx_sh);
+    route_token<EB>(lsh + grp * EB, static_cast<const float*>(bsh), E, k, route_scale, lane16, true, grp, idx,
+                    idx64, wout, vout, idx_sh);
   __syncthreads();
 
   // 3. dispatch: rank slot s among the earlier slots with the same expert
@@ -543,14 +552,7 @@ __global__ __launch_bounds__(kTinyThreads) void route_dispatch_tiny_kernel(
     pending &= ~m;
   }
   __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int q = 0; q < E; ++q) {
-      start[q] = run;
-      for (int w = 0; w < kTinyWaves; ++w) run += wcount[w][q];
-    }
-    start[E] = run;
-  }
+  scan_wave_counts<kTinyWaves>(wcount, E, start);
   __syncthreads();
   if (valid) {
     int pos = start[e] + rank;
