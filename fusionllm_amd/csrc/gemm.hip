@@ -1105,14 +1105,6 @@ __device__ __forceinline__ void group_rows(const WgradArgs& a, int g, int& row_b
   }
 }
 
-__device__ __forceinline__ void store_grad(const WgradArgs& a, int g, int m, int n, float v) {
-  const int64_t o = (m < a.m_split) ? static_cast<int64_t>(m) * a.n_out + n
-                                    : static_cast<int64_t>(m - a.m_split) * a.n_out + n;
-  void* base = (m < a.m_split) ? a.out_lo[g] : a.out_hi[g];
-  if (a.out_dtype == FMOE_BF16) static_cast<uint16_t*>(base)[o] = f2bf(v);
-  else static_cast<float*>(base)[o] = v;
-}
-
 // ---- weight gradients on the shared core ------------------------------------
 // Both operands are MN-contiguous ([rows, m_out] and [rows, n_out]), so their
 // 64 x 256 stage tiles are copied as they lie in memory (K-major: 64 k rows of
@@ -1376,44 +1368,67 @@ __global__ __launch_bounds__(core::NT, 1) void wgrad_tr_kernel(const WgradArgs a
 }
 
 // Adds the chunk partials of each multi-chunk group in chunk order; 8
-// consecutive outputs per thread (m_out * n_out is a multiple of 64).  A
-// group without rows gets a zero gradient (no work unit of the product
-// kernel writes it).
+// consecutive outputs of one row per thread (m_out and n_out are multiples of
+// 64), written with 16-byte stores.  The loads of kWgradReduceBatch chunks are
+// issued together (a loop that waited for each chunk's loads before the next
+// paid one memory latency per chunk); the sums still run in chunk order,
+// from 0.  A group without rows gets a zero gradient (no work unit of the
+// product kernel writes it).
+constexpr int kWgradReduceBatch = 8;
+
+__device__ __forceinline__ void store_grad8(const WgradArgs& a, int g, int64_t i0, const float (&v)[8]) {
+  const int m = static_cast<int>(i0 / a.n_out), n = static_cast<int>(i0 - static_cast<int64_t>(m) * a.n_out);
+  const bool lo = m < a.m_split;
+  const int64_t o = static_cast<int64_t>(lo ? m : m - a.m_split) * a.n_out + n;
+  void* base = lo ? a.out_lo[g] : a.out_hi[g];
+  if (a.out_dtype == FMOE_BF16) {
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + o) = pack8(v);
+  } else {
+    float4* dst = reinterpret_cast<float4*>(static_cast<float*>(base) + o);
+    dst[0] = make_float4(v[0], v[1], v[2], v[3]);
+    dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const WgradArgs args) {
   const int g = blockIdx.y;
   int row_base, M;
   group_rows(args, g, row_base, M);
   const int chunks = (M + args.kc - 1) / args.kc;
-  if (chunks == 0) {
-    const int64_t mn = static_cast<int64_t>(args.m_out) * args.n_out;
-    const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
-    if (i0 >= mn) return;
-    const int m = static_cast<int>(i0 / args.n_out), n = static_cast<int>(i0 % args.n_out);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) store_grad(args, g, m, n + e, 0.0f);
-    return;
-  }
-  if (chunks <= 1) return;
-  int pbase = 0;
-  for (int q = 0; q < g; ++q) {
-    int rb, Mq;
-    group_rows(args, q, rb, Mq);
-    const int cq = (Mq + args.kc - 1) / args.kc;
-    if (cq > 1) pbase += cq;
-  }
   const int64_t mn = static_cast<int64_t>(args.m_out) * args.n_out;
   const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
-  if (i0 >= mn) return;
+  if (i0 >= mn || chunks == 1) return;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int c = 0; c < chunks; ++c) {
-    const float4* src = reinterpret_cast<const float4*>(args.partial + (pbase + c) * mn + i0);
-    const float4 u = src[0], v = src[1];
-    acc[0] = acc[0] + u.x; acc[1] = acc[1] + u.y; acc[2] = acc[2] + u.z; acc[3] = acc[3] + u.w;
-    acc[4] = acc[4] + v.x; acc[5] = acc[5] + v.y; acc[6] = acc[6] + v.z; acc[7] = acc[7] + v.w;
-  }
-  const int m = static_cast<int>(i0 / args.n_out), n = static_cast<int>(i0 % args.n_out);
+  if (chunks > 1) {
+    int pbase = 0;
+    for (int q = 0; q < g; ++q) {
+      int rb, Mq;
+      group_rows(args, q, rb, Mq);
+      const int cq = (Mq + args.kc - 1) / args.kc;
+      if (cq > 1) pbase += cq;
+    }
+    const float* src0 = args.partial + static_cast<int64_t>(pbase) * mn + i0;
+    for (int c0 = 0; c0 < chunks; c0 += kWgradReduceBatch) {
+      float4 u[kWgradReduceBatch][2];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) store_grad(args, g, m, n + e, acc[e]);
+      for (int b = 0; b < kWgradReduceBatch; ++b) {
+        // chunks past the last re-read the last one and are not added
+        const float4* src = reinterpret_cast<const float4*>(src0 + min(c0 + b, chunks - 1) * mn);
+        u[b][0] = src[0];
+        u[b][1] = src[1];
+      }
+#pragma unroll
+      for (int b = 0; b < kWgradReduceBatch; ++b) {
+        if (c0 + b < chunks) {
+          acc[0] = acc[0] + u[b][0].x; acc[1] = acc[1] + u[b][0].y;
+          acc[2] = acc[2] + u[b][0].z; acc[3] = acc[3] + u[b][0].w;
+          acc[4] = acc[4] + u[b][1].x; acc[5] = acc[5] + u[b][1].y;
+          acc[6] = acc[6] + u[b][1].z; acc[7] = acc[7] + u[b][1].w;
+        }
+      }
+    }
+  }
+  store_grad8(args, g, i0, acc);
 }
 
 // ---- host side --------------------------------------------------------------
@@ -1747,6 +1762,7 @@ extern "C" int fmoe_weight_grad(const void* a_routed, const void* a_shared, int6
   const int G = n_experts + (rows_shared > 0 ? 1 : 0);
   for (int g = 0; g < G; ++g) {
     if (!out_lo[g] || (m_split < m_out && !out_hi[g])) return FMOE_ERR_INVALID_ARG;
+    if (!aligned16(out_lo[g]) || (m_split < m_out && !aligned16(out_hi[g]))) return FMOE_ERR_ALIGN;
     a.out_lo[g] = out_lo[g];
     a.out_hi[g] = (m_split < m_out) ? out_hi[g] : nullptr;
   }

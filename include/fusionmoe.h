@@ -261,7 +261,8 @@ int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int n_experts,
  *   G_e = A_e^T B_e,  A_e = rows of expert e of A ([*, m_out]),
  *                     B_e = the same rows of B ([*, n_out]).
  * Row i < m_split of G_e goes to out_lo[e] ([m_split, n_out]); rows >= m_split
- * go to out_hi[e] ([m_out - m_split, n_out]).  out dtype bf16 or f32.
+ * go to out_hi[e] ([m_out - m_split, n_out]).  out dtype bf16 or f32; every
+ * out_lo[e] / out_hi[e] 16-byte aligned (else FMOE_ERR_ALIGN).
  * For w2: A = d_out, B = h, m_split = m_out = dim.  For w1/w3: A = d_ab,
  * B = x, m_split = inter (out_lo = dw1, out_hi = dw3).  With b_gather
  * non-null, b_routed is the token rows x [gather_tokens, n_out] and routed
