@@ -87,17 +87,25 @@ __device__ __forceinline__ void pick_topk(const float (&s)[EB], int E, int k, fl
   }
 }
 
-// Scores and top-k of one token from its logits lg[0 .. E) (bias not yet
-// added), the scores also computed redundantly by the group's 16 lanes.
+// Scores and top-k of one token from its logits lg[0 .. E) in LDS (bias not
+// yet added; overwritten with the scores).  Lane l of the token's 16-lane
+// group forms the scores of experts l, l + 16, ... (one exp and one divide
+// each: every lane forming all E of them in turn took 2.7 us at E = 8), then
+// each lane reads all E scores back for the top-k.  The group's lanes are in
+// one wave, whose LDS accesses complete in program order.
 template <int EB, typename BiasT>
-__device__ __forceinline__ void route_token(const float* lg, const BiasT* bg, int E, int k,
+__device__ __forceinline__ void route_token(float* lg, const BiasT* bg, int E, int k,
                                             float route_scale, int lane16, bool active, int t,
                                             int32_t* __restrict__ idx, int64_t* __restrict__ idx64,
                                             float* __restrict__ wout, float* __restrict__ vout,
                                             int* idx_lds = nullptr, int* hist_lds = nullptr) {
+  for (int e = lane16; e < E; e += kRouterLanes) lg[e] = fm_sigmoid(lg[e] + bias_at(bg, e));
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   float s[EB];
 #pragma unroll
-  for (int e = 0; e < EB; ++e) s[e] = (e < E) ? fm_sigmoid(lg[e] + bias_at(bg, e)) : 0.0f;
+  for (int e = 0; e < EB; ++e) s[e] = (e < E) ? lg[e] : 0.0f;
   pick_topk<EB>(s, E, k, route_scale, lane16, active, t, idx, idx64, wout, vout, idx_lds, hist_lds);
 }
 
