@@ -74,6 +74,14 @@ def test_argument_errors_without_gpu():
                                    None, 0, None, None, None, 0, None) == 1  # null inputs
     assert lib.fmoe_weight_grad(None, None, 8, None, None, 8, None, 0, 0, None, 1, 10, 0, 128, 128, 0, pp, None,
                                 0, None, 0, None) == 2
+    # weight gradients: every output 16-byte aligned (the chunk reduction writes 8 outputs per store),
+    # checked before anything is launched
+    ws = lib.fmoe_weight_grad_workspace_bytes(64, 0, 1, 128, 128)
+    odd, even = _lib.ptr_array([fake + 8]), _lib.ptr_array([fake])
+    assert lib.fmoe_weight_grad(fake, None, 128, fake, None, 128, None, 0, 0, fake, 1, 64, 0, 128, 128, 128, odd,
+                                None, 0, fake, ws, None) == 3
+    assert lib.fmoe_weight_grad(fake, None, 128, fake, None, 128, None, 0, 0, fake, 1, 64, 0, 128, 128, 64, even,
+                                odd, 0, fake, ws, None) == 3
     # one-launch bf16 casts: count and sizes checked before any pointer is used
     n1 = (ctypes.c_int64 * 1)(-1)
     assert lib.fmoe_cast_bf16(pp, pp, n1, 1, None) == 1
