@@ -1455,6 +1455,19 @@ int check_common(int n_experts, int64_t rows_routed, int64_t rows_shared, int64_
   return FMOE_OK;
 }
 
+// The four row products.  Their tile copies address a lane's operand row
+// with a 32-bit byte offset from the tile's base: up to 255 rows of at most
+// 2 * inter (or dim) elements for the activations, any row of the weight for
+// the forward products (n * K + 56 < dim * inter elements).  So a row holds
+// fewer than 2^22 elements and a weight matrix fewer than 2^31.
+int check_row_product(int n_experts, int64_t rows_routed, int64_t rows_shared, int64_t dim, int64_t inter) {
+  const int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
+  if (st) return st;
+  constexpr int64_t kMaxRow = int64_t(1) << 22;
+  if (dim >= kMaxRow || inter >= kMaxRow || dim * inter >= (int64_t(1) << 31)) return FMOE_ERR_SHAPE;
+  return FMOE_OK;
+}
+
 // Row counts up to which a launch sends groups of <= kSmallM rows to the
 // small-group kernel (decode-sized batches); larger launches use the tiled
 // kernel for every group.
@@ -1571,7 +1584,7 @@ extern "C" int fmoe_gateup_fwd(const void* x_routed, const int32_t* gather, int 
                                int n_experts, int64_t rows_routed, int64_t rows_shared, int64_t dim,
                                int64_t inter, const void* const* w1, const void* const* w3,
                                void* ab, void* h, void* workspace, size_t workspace_bytes, void* stream) {
-  int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
+  int st = check_row_product(n_experts, rows_routed, rows_shared, dim, inter);
   if (st) return st;
   if (rows_routed + rows_shared == 0) return FMOE_OK;
   if (!offsets || !w1 || !w3 || !ab || !h || (rows_routed && !x_routed) ||
@@ -1616,7 +1629,7 @@ extern "C" int fmoe_down_fwd(const void* h, const int32_t* offsets, int n_expert
                              int64_t rows_routed, int64_t rows_shared, int64_t dim, int64_t inter,
                              const void* const* w2, void* out, void* workspace, size_t workspace_bytes,
                              void* stream) {
-  int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
+  int st = check_row_product(n_experts, rows_routed, rows_shared, dim, inter);
   if (st) return st;
   if (rows_routed + rows_shared == 0) return FMOE_OK;
   if (!h || !offsets || !w2 || !out) return FMOE_ERR_INVALID_ARG;
@@ -1646,7 +1659,7 @@ extern "C" int fmoe_down_bwd_dx(const void* d_out_routed, const void* d_out_shar
                                 int64_t rows_shared, int64_t dim, int64_t inter, const void* const* w2,
                                 const void* ab, void* d_ab, void* workspace, size_t workspace_bytes,
                                 void* stream) {
-  int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
+  int st = check_row_product(n_experts, rows_routed, rows_shared, dim, inter);
   if (st) return st;
   if (rows_routed + rows_shared == 0) return FMOE_OK;
   if (!offsets || !w2 || !ab || !d_ab || (rows_routed && !d_out_routed) ||
@@ -1680,7 +1693,7 @@ extern "C" int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int 
                                   int64_t rows_routed, int64_t rows_shared, int64_t dim,
                                   int64_t inter, const void* const* w1, const void* const* w3, void* dx_rows,
                                   void* workspace, size_t workspace_bytes, void* stream) {
-  int st = check_common(n_experts, rows_routed, rows_shared, dim, inter);
+  int st = check_row_product(n_experts, rows_routed, rows_shared, dim, inter);
   if (st) return st;
   if (rows_routed + rows_shared == 0) return FMOE_OK;
   if (!d_ab || !offsets || !w1 || !w3 || !dx_rows) return FMOE_ERR_INVALID_ARG;
@@ -1745,6 +1758,10 @@ extern "C" int fmoe_weight_grad(const void* a_routed, const void* a_shared, int6
   if (!offsets || !out_lo || (m_split < m_out && !out_hi) || (rows_routed && (!a_routed || !b_routed)))
     return FMOE_ERR_INVALID_ARG;
   if (lda % 8 != 0 || ldb % 8 != 0) return FMOE_ERR_ALIGN;
+  // rows of at least m_out (n_out) elements; the stage copies address up to
+  // 63 rows past a stage's first with a 32-bit byte offset
+  if (lda < m_out || ldb < n_out || lda >= (int64_t(1) << 24) || ldb >= (int64_t(1) << 24))
+    return FMOE_ERR_SHAPE;
   if (workspace_bytes < fmoe_weight_grad_workspace_bytes(rows_routed, rows_shared, n_experts, m_out, n_out))
     return FMOE_ERR_WORKSPACE;
   if (!workspace) return FMOE_ERR_INVALID_ARG;

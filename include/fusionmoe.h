@@ -30,6 +30,9 @@
  *     rows_shared > 0).  Each weight is the nn.Linear weight of the
  *     reference: w1, w3 are [inter, dim], w2 is [dim, inter].
  *   - dim and inter must be multiples of 64; n_experts <= FMOE_MAX_EXPERTS.
+ *     The four row products (fmoe_gateup_fwd, fmoe_down_fwd, fmoe_down_bwd_dx,
+ *     fmoe_gateup_bwd_dx) also need dim, inter < 2^22 and dim * inter < 2^31
+ *     (their tile copies form 32-bit byte offsets), else FMOE_ERR_SHAPE.
  */
 #ifndef FUSIONMOE_H
 #define FUSIONMOE_H
@@ -262,7 +265,8 @@ int fmoe_gateup_bwd_dx(const void* d_ab, const int32_t* offsets, int n_experts,
  *                     B_e = the same rows of B ([*, n_out]).
  * Row i < m_split of G_e goes to out_lo[e] ([m_split, n_out]); rows >= m_split
  * go to out_hi[e] ([m_out - m_split, n_out]).  out dtype bf16 or f32; every
- * out_lo[e] / out_hi[e] 16-byte aligned (else FMOE_ERR_ALIGN).
+ * out_lo[e] / out_hi[e] 16-byte aligned (else FMOE_ERR_ALIGN); m_out <= lda < 2^24,
+ * n_out <= ldb < 2^24 (else FMOE_ERR_SHAPE).
  * For w2: A = d_out, B = h, m_split = m_out = dim.  For w1/w3: A = d_ab,
  * B = x, m_split = inter (out_lo = dw1, out_hi = dw3).  With b_gather
  * non-null, b_routed is the token rows x [gather_tokens, n_out] and routed

@@ -58,6 +58,16 @@ def test_argument_errors_without_gpu():
                                None) == 2
     assert lib.fmoe_gateup_fwd(None, None, 0, 0, None, None, 1, 10, 0, 128, 128, pp, pp, None, None, None, 0,
                                None) == 1
+    # the row products' 32-bit copy offsets: rows below 2^22 elements, a weight below 2^31
+    assert lib.fmoe_gateup_fwd(None, None, 0, 0, None, None, 1, 10, 0, 1 << 16, 1 << 15, pp, pp, None, None, None,
+                               0, None) == 2
+    assert lib.fmoe_gateup_fwd(None, None, 0, 0, None, None, 1, 10, 0, 1 << 22, 64, pp, pp, None, None, None, 0,
+                               None) == 2
+    assert lib.fmoe_gateup_fwd(None, None, 0, 0, None, None, 1, 10, 0, (1 << 22) - 64, 64, pp, pp, None, None,
+                               None, 0, None) == 1  # admitted (then the null pointers)
+    assert lib.fmoe_down_fwd(None, None, 1, 10, 0, 64, 1 << 22, pp, None, None, 0, None) == 2
+    assert lib.fmoe_down_bwd_dx(None, None, None, 1, 10, 0, 1 << 16, 1 << 15, pp, None, None, None, 0, None) == 2
+    assert lib.fmoe_gateup_bwd_dx(None, None, 1, 10, 0, 1 << 15, 1 << 16, pp, pp, None, None, 0, None) == 2
     assert lib.fmoe_combine_fwd(None, None, None, None, 4, 768, 2, 8, 1, 5, None, None, None) == 4
     # RMSNorm around the block
     assert lib.fmoe_rmsnorm_fwd(None, 0, None, 0, 4, 100, 1e-6, None, None, None) == 2
@@ -82,6 +92,11 @@ def test_argument_errors_without_gpu():
                                 None, 0, fake, ws, None) == 3
     assert lib.fmoe_weight_grad(fake, None, 128, fake, None, 128, None, 0, 0, fake, 1, 64, 0, 128, 128, 64, even,
                                 odd, 0, fake, ws, None) == 3
+    # leading dimensions: at least the row length, below 2^24 (32-bit copy offsets)
+    assert lib.fmoe_weight_grad(fake, None, 64, fake, None, 128, None, 0, 0, fake, 1, 64, 0, 128, 128, 128, even,
+                                None, 0, fake, ws, None) == 2
+    assert lib.fmoe_weight_grad(fake, None, 128, fake, None, 1 << 24, None, 0, 0, fake, 1, 64, 0, 128, 128, 128,
+                                even, None, 0, fake, ws, None) == 2
     # one-launch bf16 casts: count and sizes checked before any pointer is used
     n1 = (ctypes.c_int64 * 1)(-1)
     assert lib.fmoe_cast_bf16(pp, pp, n1, 1, None) == 1
